@@ -1,0 +1,294 @@
+// Decoder-side tagged ops: MSDeformAttn sampling (op 2), mask -> box (op 1)
+// and top-300 query selection (op 13).
+//
+// Semantics follow the reference's CPU ops, which define the results:
+// op_msdeform (src/ppdoclayout.cpp:148-198), op_mask_box (:100-140),
+// op_topk300 (:75-96).  Float contraction is off in this file so every
+// multiply and add rounds where the CPU op's source rounds, except the
+// explicit fmaf of the sampling accumulation (one fused multiply-add per
+// corner tap, the reference GPU kernel's numerical contract).
+#include "ppdl_internal.h"
+
+#pragma clang fp contract(off)
+
+namespace ppdl {
+namespace {
+
+__constant__ int kLvlW[3] = {100, 50, 25};
+__constant__ int kLvlStart[3] = {0, 10000, 12500};
+
+// ---------------------------------------------------------------------------
+// MSDeformAttn: one 256-thread block per query; wave w serves heads 2w, 2w+1
+// (lane>>5 picks the head, lane&31 the channel).  For a fixed (head, point,
+// corner) the 32 lanes of a head read 32 consecutive floats of the value map,
+// so every gather is one 128-byte segment.
+//   val  (13125, 256) token-major       off (NQ, 192) [((h*3+l)*4+p)*2+xy]
+//   awr  (NQ, 96) pre-softmax [h*12 + l*4 + p]   ref (NQ, 4) cxcywh
+__global__ __launch_bounds__(256) void k_msdeform(const float *__restrict__ val,
+                                                  const float *__restrict__ off,
+                                                  const float *__restrict__ awr,
+                                                  const float *__restrict__ ref,
+                                                  float *__restrict__ out, int nq) {
+    const int q = blockIdx.x;
+    if (q >= nq) return;
+    const int h = threadIdx.x >> 5, c = threadIdx.x & 31;
+    const float rx = ref[q * 4 + 0], ry = ref[q * 4 + 1];
+    const float rw = ref[q * 4 + 2], rh = ref[q * 4 + 3];
+
+    const float *a = awr + (int64_t)q * 96 + h * 12;
+    float w[12];
+    float amax = a[0];
+#pragma unroll
+    for (int i = 1; i < 12; i++) amax = fmaxf(amax, a[i]);
+    float wsum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 12; i++) {
+        w[i] = expf(a[i] - amax);
+        wsum += w[i];
+    }
+#pragma unroll
+    for (int i = 0; i < 12; i++) w[i] /= wsum;
+
+    const float *o = off + (int64_t)q * 192 + h * 24;
+    const float *vh = val + h * kHD + c;
+    float acc = 0.0f;
+#pragma unroll
+    for (int l = 0; l < 3; l++) {
+        const int W = kLvlW[l], H = kLvlW[l], st = kLvlStart[l];
+#pragma unroll
+        for (int p = 0; p < 4; p++) {
+            const float ox = o[(l * 4 + p) * 2 + 0];
+            const float oy = o[(l * 4 + p) * 2 + 1];
+            const float lx = rx + ox / 4.0f * rw * 0.5f;
+            const float ly = ry + oy / 4.0f * rh * 0.5f;
+            // grid_sample bilinear, zero padding, align_corners = false.  The
+            // clamp only keeps the float->int conversion defined: any sample
+            // beyond it has both corner columns (rows) outside the map.
+            const float fx = fminf(fmaxf(lx * (float)W - 0.5f, -2.0f), (float)W + 1.0f);
+            const float fy = fminf(fmaxf(ly * (float)H - 0.5f, -2.0f), (float)H + 1.0f);
+            const int x0 = (int)floorf(fx), y0 = (int)floorf(fy);
+            const float tx = fx - (float)x0, ty = fy - (float)y0;
+            const float wt = w[l * 4 + p];
+            const float cw[4] = {(1.0f - tx) * (1.0f - ty), tx * (1.0f - ty), (1.0f - tx) * ty, tx * ty};
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const int xx = x0 + (k & 1), yy = y0 + (k >> 1);
+                if (xx < 0 || xx >= W || yy < 0 || yy >= H || cw[k] == 0.0f) continue;
+                const float ww = wt * cw[k];
+                acc = fmaf(ww, vh[(int64_t)(st + yy * W + xx) * kDM], acc);
+            }
+        }
+    }
+    out[(int64_t)q * kDM + h * kHD + c] = acc;
+}
+
+// ---------------------------------------------------------------------------
+// mask -> box: per query, the bounding box of pixels with logit > 0 on the
+// 200x200 mask, as inverse-sigmoid cxcywh normalised by 200.
+__device__ __forceinline__ float invsig(float x) {
+    x = fminf(fmaxf(x, 0.0f), 1.0f);
+    const float x1 = fmaxf(x, 1e-5f);
+    const float x2 = fmaxf(1.0f - x, 1e-5f);
+    return logf(x1 / x2);
+}
+
+__global__ __launch_bounds__(256) void k_mask_box(const float *__restrict__ ml,
+                                                  float *__restrict__ out, int nq) {
+    const int q = blockIdx.x;
+    if (q >= nq) return;
+    const float4 *m4 = reinterpret_cast<const float4 *>(ml + (int64_t)q * kMaskPix);
+    int xmin = kMaskHW, xmax = -1, ymin = kMaskHW, ymax = -1;
+    for (int i = threadIdx.x; i < kMaskPix / 4; i += 256) {
+        const float4 v = m4[i];
+        const int y = (4 * i) / kMaskHW, x = 4 * i - y * kMaskHW;  // 200 % 4 == 0: same row
+        const float e[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            if (e[j] > 0.0f) {
+                xmin = min(xmin, x + j);
+                xmax = max(xmax, x + j);
+                ymin = min(ymin, y);
+                ymax = max(ymax, y);
+            }
+        }
+    }
+#pragma unroll
+    for (int s = 32; s > 0; s >>= 1) {
+        xmin = min(xmin, __shfl_xor(xmin, s));
+        xmax = max(xmax, __shfl_xor(xmax, s));
+        ymin = min(ymin, __shfl_xor(ymin, s));
+        ymax = max(ymax, __shfl_xor(ymax, s));
+    }
+    __shared__ int red[4][4];
+    const int wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) {
+        red[wave][0] = xmin;
+        red[wave][1] = xmax;
+        red[wave][2] = ymin;
+        red[wave][3] = ymax;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < 4; w++) {
+            xmin = min(xmin, red[w][0]);
+            xmax = max(xmax, red[w][1]);
+            ymin = min(ymin, red[w][2]);
+            ymax = max(ymax, red[w][3]);
+        }
+        float bx0, by0, bx1, by1;
+        if (xmax < 0) {
+            bx0 = by0 = bx1 = by1 = 0.0f;
+        } else {
+            bx0 = (float)xmin;
+            by0 = (float)ymin;
+            bx1 = (float)xmax + 1.0f;
+            by1 = (float)ymax + 1.0f;
+        }
+        bx0 /= (float)kMaskHW;
+        bx1 /= (float)kMaskHW;
+        by0 /= (float)kMaskHW;
+        by1 /= (float)kMaskHW;
+        const float cx = (bx0 + bx1) * 0.5f, cy = (by0 + by1) * 0.5f;
+        const float bw = bx1 - bx0, bh = by1 - by0;
+        float *o = out + (int64_t)q * 4;
+        o[0] = invsig(cx);
+        o[1] = invsig(cy);
+        o[2] = invsig(bw);
+        o[3] = invsig(bh);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// top-NQ tokens by max-class logit, descending, ties to the lower index.
+// Each token gets a unique 64-bit key: order-preserving float bits (with -0
+// folded into +0, since the CPU comparison treats them as equal) in the high
+// word and the bit-inverted index in the low word, so "larger key" is exactly
+// the CPU order.  A radix select over the 8 key bytes finds the NQ-th largest
+// key; the keys at or above it are gathered and bitonic-sorted in LDS.
+constexpr int kTopkThreads = 1024;
+constexpr int kTopkPer = 13;  // 13 * 1024 = 13312 >= 13125
+constexpr int kTopkSort = 512;
+
+__device__ __forceinline__ uint64_t topk_key(float m, int idx) {
+    m = m + 0.0f;  // -0 -> +0
+    uint32_t u = __float_as_uint(m);
+    u ^= (u >> 31) ? 0xFFFFFFFFu : 0x80000000u;
+    return ((uint64_t)u << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)idx);
+}
+
+__global__ __launch_bounds__(kTopkThreads) void k_topk(const float *__restrict__ lg,
+                                                       int32_t *__restrict__ out, int ntok, int nc,
+                                                       int nq) {
+    __shared__ uint32_t hist[256];
+    __shared__ uint64_t sel[kTopkSort];
+    __shared__ int s_digit, s_rank, s_cnt;
+    const int tid = threadIdx.x;
+
+    uint64_t key[kTopkPer];
+#pragma unroll
+    for (int j = 0; j < kTopkPer; j++) {
+        const int t = tid + j * kTopkThreads;
+        key[j] = 0;  // below every real key (real keys have a nonzero low word or high word)
+        if (t < ntok) {
+            const float *p = lg + (int64_t)t * nc;
+            float m = p[0];
+            for (int c = 1; c < nc; c++) m = (m < p[c]) ? p[c] : m;
+            key[j] = topk_key(m, t);
+        }
+    }
+
+    // radix select: after the loop, `prefix` is the NQ-th largest key
+    uint64_t prefix = 0, mask = 0;
+    int rank = nq;  // 1-based rank still to find within the current prefix
+    for (int byte = 7; byte >= 0; byte--) {
+        for (int i = tid; i < 256; i += kTopkThreads) hist[i] = 0;
+        __syncthreads();
+        const int sh = byte * 8;
+#pragma unroll
+        for (int j = 0; j < kTopkPer; j++)
+            if ((key[j] & mask) == prefix && key[j] != 0) atomicAdd(&hist[(key[j] >> sh) & 0xFF], 1u);
+        __syncthreads();
+        if (tid < 64) {
+            // wave 0 scans the 256 bins from the top: 4 bins per lane
+            uint32_t c4[4], tot = 0;
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                c4[b] = hist[255 - (tid * 4 + b)];
+                tot += c4[b];
+            }
+            uint32_t incl = tot;  // inclusive prefix over lanes (top bins first)
+#pragma unroll
+            for (int s = 1; s < 64; s <<= 1) {
+                const uint32_t v = __shfl_up(incl, s);
+                if (tid >= s) incl += v;
+            }
+            uint32_t run = incl - tot;
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                if (run < (uint32_t)rank && run + c4[b] >= (uint32_t)rank) {
+                    s_digit = 255 - (tid * 4 + b);
+                    s_rank = rank - (int)run;
+                }
+                run += c4[b];
+            }
+        }
+        __syncthreads();
+        prefix |= (uint64_t)s_digit << sh;
+        mask |= (uint64_t)0xFF << sh;
+        rank = s_rank;
+        __syncthreads();
+    }
+
+    // gather keys >= threshold (exactly nq of them: keys are unique)
+    for (int i = tid; i < kTopkSort; i += kTopkThreads) sel[i] = 0;
+    if (tid == 0) s_cnt = 0;
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < kTopkPer; j++) {
+        if (key[j] != 0 && key[j] >= prefix) {
+            const int pos = atomicAdd(&s_cnt, 1);
+            if (pos < kTopkSort) sel[pos] = key[j];
+        }
+    }
+    __syncthreads();
+
+    // bitonic sort, descending
+    for (int k = 2; k <= kTopkSort; k <<= 1) {
+        for (int j = k >> 1; j > 0; j >>= 1) {
+            for (int i = tid; i < kTopkSort; i += kTopkThreads) {
+                const int ixj = i ^ j;
+                if (ixj > i) {
+                    const uint64_t a = sel[i], b = sel[ixj];
+                    const bool desc = (i & k) == 0;
+                    if (desc ? (a < b) : (a > b)) {
+                        sel[i] = b;
+                        sel[ixj] = a;
+                    }
+                }
+            }
+            __syncthreads();
+        }
+    }
+    for (int r = tid; r < nq; r += kTopkThreads)
+        out[r] = (int32_t)(0xFFFFFFFFu - (uint32_t)(sel[r] & 0xFFFFFFFFu));
+}
+
+}  // namespace
+
+hipError_t msdeform(const float *val, const float *off, const float *awr, const float *ref,
+                    float *out, int nq, hipStream_t s) {
+    hipLaunchKernelGGL(k_msdeform, dim3(nq), dim3(256), 0, s, val, off, awr, ref, out, nq);
+    return hipGetLastError();
+}
+
+hipError_t mask_box(const float *ml, float *out, int nq, hipStream_t s) {
+    hipLaunchKernelGGL(k_mask_box, dim3(nq), dim3(256), 0, s, ml, out, nq);
+    return hipGetLastError();
+}
+
+hipError_t topk(const float *logits, int32_t *out, int ntok, int nc, int nq, hipStream_t s) {
+    hipLaunchKernelGGL(k_topk, dim3(1), dim3(kTopkThreads), 0, s, logits, out, ntok, nc, nq);
+    return hipGetLastError();
+}
+
+}  // namespace ppdl

@@ -1,0 +1,88 @@
+// Internal declarations shared by the HIP kernels and the C-ABI dispatcher.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ppdl {
+
+// ---- model geometry fixed by PP-DocLayoutV3 (src/ppdoclayout.cpp:31-44) ----
+constexpr int kDM = 256;           // d_model
+constexpr int kNH = 8;             // attention heads
+constexpr int kHD = 32;            // head dim
+constexpr int kNLVL = 3;           // feature levels
+constexpr int kNPTS = 4;           // sampling points per level
+constexpr int kNTOK = 13125;       // 100^2 + 50^2 + 25^2 value tokens
+constexpr int kMaskHW = 200;       // mask side
+constexpr int kMaskPix = kMaskHW * kMaskHW;
+
+// ---- Winograd F(4,3), Toom-Cook points {0, 1, -1, 2, -1/2, inf} ----
+// Convention: Y = At [ (G g G^T) (.) (Bt d Bt^T) ] At^T over 6x6 input tiles
+// with stride 4.  Bt and At hold dyadic rationals (exact in FP32); G holds
+// thirds and fifteenths and is applied in float64 at repack time only.
+// Chosen over {0,+-1,+-2} for a ~2.5x smaller FP32 error on 256-channel convs.
+constexpr float kBt[6][6] = {
+    {1.0f, 1.5f, -2.0f, -1.5f, 1.0f, 0.0f},
+    {0.0f, -1.0f, -2.5f, -0.5f, 1.0f, 0.0f},
+    {0.0f, 1.0f, 0.5f, -2.5f, 1.0f, 0.0f},
+    {0.0f, -0.5f, -1.0f, 0.5f, 1.0f, 0.0f},
+    {0.0f, 2.0f, -1.0f, -2.0f, 1.0f, 0.0f},
+    {0.0f, 1.0f, 1.5f, -2.0f, -1.5f, 1.0f},
+};
+constexpr float kAt[4][6] = {
+    {1.0f, 1.0f, 1.0f, 1.0f, 1.0f, 0.0f},
+    {0.0f, 1.0f, -1.0f, 2.0f, -0.5f, 0.0f},
+    {0.0f, 1.0f, 1.0f, 4.0f, 0.25f, 0.0f},
+    {0.0f, 1.0f, -1.0f, 8.0f, -0.125f, 1.0f},
+};
+constexpr double kG[6][3] = {
+    {1.0, 0.0, 0.0},
+    {-1.0 / 3.0, -1.0 / 3.0, -1.0 / 3.0},
+    {1.0 / 3.0, -1.0 / 3.0, 1.0 / 3.0},
+    {1.0 / 15.0, 2.0 / 15.0, 4.0 / 15.0},
+    {-16.0 / 15.0, 8.0 / 15.0, -4.0 / 15.0},
+    {0.0, 0.0, 1.0},
+};
+
+// ---- GEMM core: C[m][n] = epi( sum_k At[k][m] * B[k][n] ) ----
+// A is stored k-major (element (m,k) at A[k*lda + m]); B is either a dense
+// k-major matrix or an implicit im2col view of a CHW image.
+struct GemmArgs {
+    const float *A;
+    int64_t lda, sA;  // sA: batch stride (elements)
+    const float *B;
+    int64_t ldb, sB;
+    float *C;
+    int64_t ldc, sC;
+    const float *bias;  // per-m bias or nullptr
+    int M, N, K, batch, act;
+    // implicit im2col geometry: B[k][n] = x[ic][oy*S-P+kh][ox*S-P+kw],
+    // k = (kh*KW + kw)*IC + ic, n = oy*OW + ox
+    int IC, IH, IW, OW, KW, S, P;
+};
+
+hipError_t gemm_dense(const GemmArgs &g, hipStream_t s);
+hipError_t gemm_im2col(const GemmArgs &g, hipStream_t s);
+
+// ---- Winograd transforms ----
+// pad: 0 when x is already padded (op 10), 1 when the conv's pad is fused.
+hipError_t wg4_input(const float *x, float *dt, int IW, int IH, int IC, int TW, int TH, int pad,
+                     hipStream_t s);
+hipError_t wg4_output(const float *yt, const float *bias, float *out, int TW, int TH, int OC,
+                      int OW, int OH, int act, hipStream_t s);
+
+// ---- elementwise / data movement ----
+hipError_t bias_act(const float *in, const float *bias, float *out, int64_t n, int64_t plane,
+                    int act, hipStream_t s);
+hipError_t im2col_ggml(const float *x, float *dst, int64_t IW, int64_t IH, int64_t OW, int64_t OH,
+                       int64_t KW, int64_t KH, int64_t IC, int64_t N, int64_t ch_stride,
+                       int64_t img_stride, int s0, int s1, int p0, int p1, int d0, int d1,
+                       hipStream_t s);
+
+// ---- decoder ops ----
+hipError_t msdeform(const float *val, const float *off, const float *awr, const float *ref,
+                    float *out, int nq, hipStream_t s);
+hipError_t mask_box(const float *ml, float *out, int nq, hipStream_t s);
+hipError_t topk(const float *logits, int32_t *out, int ntok, int nc, int nq, hipStream_t s);
+
+}  // namespace ppdl

@@ -1,0 +1,386 @@
+"""GPU parity of every tagged op, called through the C-ABI (libppdl_hip.so).
+
+Each test runs the HIP path on seeded inputs and compares it with the CPU
+oracle on the same inputs:
+  * conv outputs (1x1 GEMM, Winograd F(4,3), implicit-im2col GEMM) and the
+    MSDeformAttn sampler: normwise max|y-ref|/max|ref| <= 2e-5 (the per-op
+    FP32 budget), plus the float64 truth where the size allows;
+  * Winograd input transform, im2col, top-k: bit-exact (same arithmetic or
+    pure data movement); output transform bit-exact without SiLU.
+Sizes include every BASELINE config (1x1 512->256 @100^2, the Winograd sweep,
+the im2col convs, MSDeformAttn at 300 queries) plus ragged edge shapes.
+"""
+import os
+import sys
+
+import numpy as np
+import pytest
+import torch
+from conftest import normwise, rel1
+
+pytestmark = pytest.mark.gpu
+
+GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+sys.path.insert(0, GOLD)
+from fixture_inputs import msdef_value_map  # noqa: E402
+
+TOL = 2e-5
+SEED = 0x5050444C
+
+
+def say(*a):
+    print("[case]", *a, flush=True)
+
+
+@pytest.fixture(scope="module", autouse=True)
+def device():
+    assert torch.cuda.is_available(), "GPU tests need a ROCm device"
+    torch.cuda.set_device(0)
+    yield
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def conv_inputs(rng, IC, H, W, OC, K):
+    x = rng.random((IC, H, W)).astype(np.float32)
+    w = (rng.standard_normal((OC, IC, K, K)) / np.sqrt(K * K * IC)).astype(np.float32)
+    b = rng.uniform(-0.1, 0.1, OC).astype(np.float32)
+    return x, w, b
+
+
+# ---------------------------------------------------------------- HIP paths
+def hip_conv1x1(hip, x, w, b, act):
+    wr, _ = hip.repack_conv(w)
+    OC = w.shape[0]
+    xt, wt, bt = dev(x), dev(wr), dev(b)
+    out = torch.empty((OC,) + x.shape[1:], device="cuda")
+    hip.run_checked(hip.OP_CONV1X1_BA, out, [xt, wt, bt], act)
+    return out, (xt, wt, bt)
+
+
+def hip_winograd(hip, x, w, b, act, prepadded=False):
+    IC, H, W = x.shape
+    OC = w.shape[0]
+    TW, TH = (W + 3) // 4, (H + 3) // 4
+    T = TW * TH
+    _, wg4 = hip.repack_conv(w)
+    wt, bt = dev(wg4), dev(b)
+    dt = torch.empty((36, IC, T), device="cuda")
+    yt = torch.empty((36, OC, T), device="cuda")
+    out = torch.empty((OC, H, W), device="cuda")
+    if prepadded:
+        xp = np.zeros((IC, 4 * TH + 2, 4 * TW + 2), np.float32)
+        xp[:, 1:H + 1, 1:W + 1] = x
+        hip.run_checked(hip.OP_WG4_INPUT, dt, [dev(xp)], T, TH)
+    else:
+        hip.run_checked(hip.OP_WG4_INPUT_PAD, dt, [dev(x)], T, TH)
+    hip.run_checked(hip.OP_WG4_MADD, yt, [dt, wt])
+    hip.run_checked(hip.OP_WG4_OUTPUT, out, [yt, bt], act, TW)
+    return out, dt, yt, wg4
+
+
+def hip_conv_im2col(hip, x, w, b, K, S, P, act):
+    wr, _ = hip.repack_conv(w)
+    IC, IH, IW = x.shape
+    OC = w.shape[0]
+    OH, OW = (IH + 2 * P - K) // S + 1, (IW + 2 * P - K) // S + 1
+    out = torch.empty((OC, OH, OW), device="cuda")
+    hip.run_checked(hip.OP_CONV_IM2COL, out, [dev(x), dev(wr), dev(b)], K | (S << 8) | (P << 16) | (act << 24))
+    return out
+
+
+# ---------------------------------------------------------------- 1x1 conv
+def test_conv1x1_config1(hip, orc):
+    say("1x1 512->256 @100x100 relu (config 1)")
+    rng = np.random.default_rng(SEED + 1)
+    x, w, b = conv_inputs(rng, 512, 100, 100, 256, 1)
+    out, (xt, wt, bt) = hip_conv1x1(hip, x, w, b, 1)
+    y = host(out)
+    ref = orc.conv2d_ref(x, w, b, 1, 0, 1)
+    assert normwise(y, ref) < TOL, normwise(y, ref)
+    # op 3 (GEMM) then op 5 (bias+act) reproduces the fused op bit for bit
+    g = torch.empty_like(out)
+    r = torch.empty_like(out)
+    hip.run_checked(hip.OP_CONV, g, [xt, wt, bt], 1)
+    hip.run_checked(hip.OP_BIASACT, r, [g, bt], 1)
+    assert np.array_equal(host(r), y)
+    # op 3 alone is the bias-free GEMM
+    assert normwise(host(g), orc.conv2d_ref(x, w, None, 1, 0, 0)) < TOL
+
+
+@pytest.mark.parametrize("IC,H,W,OC", [
+    (1, 1, 1, 1), (3, 7, 5, 2), (17, 13, 11, 33), (64, 25, 25, 200), (48, 40, 40, 24),
+    (336, 25, 25, 64), (2176, 7, 9, 40), (32, 200, 200, 48), (5, 3, 300, 130),
+])
+@pytest.mark.parametrize("act", [0, 1, 2])
+def test_conv1x1_shapes(hip, orc, IC, H, W, OC, act):
+    say(f"1x1 {IC}->{OC} @{H}x{W} act{act}")
+    rng = np.random.default_rng(IC * 7 + H * 3 + W + OC + act)
+    x, w, b = conv_inputs(rng, IC, H, W, OC, 1)
+    out, _ = hip_conv1x1(hip, x, w, b, act)
+    y = host(out)
+    assert normwise(y, orc.conv2d_ref(x, w, b, 1, 0, act)) < TOL
+    assert normwise(y, orc.conv2d_f64(x, w, b, 1, 0, act)) < TOL
+
+
+# ---------------------------------------------------------------- Winograd F(4,3)
+WG_CONFIGS = [(256, 100, 100), (256, 50, 50), (256, 25, 25), (48, 200, 200), (96, 100, 100)]
+
+
+@pytest.mark.parametrize("C,H,W", WG_CONFIGS)
+def test_winograd_config2(hip, orc, C, H, W):
+    say(f"winograd {C}->{C} @{H}x{W} silu (config 2)")
+    rng = np.random.default_rng(SEED + 2 + C + H)
+    x, w, b = conv_inputs(rng, C, H, W, C, 3)
+    out, dt, yt, wg4 = hip_winograd(hip, x, w, b, 2)
+    y = host(out)
+    ref = orc.conv2d_ref(x, w, b, 1, 1, 2)
+    e = normwise(y, ref)
+    say(f"  normwise vs reference CPU conv path {e:.2e}")
+    assert e < TOL
+    TW, TH = (W + 3) // 4, (H + 3) // 4
+    # per-op parity
+    assert np.array_equal(host(dt), orc.wg4_input(x, TW, TH, 1)), "input transform must be bit-exact"
+    yt_h = host(yt)
+    assert normwise(yt_h, orc.wg4_madd(host(dt), wg4)) < TOL
+    out_ref = orc.wg4_output(yt_h, b, TW, TH, H, W, 2)
+    assert rel1(y, out_ref) < 1e-6
+
+
+@pytest.mark.parametrize("IC,H,W,OC", [(3, 9, 10, 2), (1, 1, 1, 1), (5, 4, 4, 7), (8, 5, 6, 3),
+                                       (33, 17, 23, 65), (128, 50, 50, 96), (64, 13, 200, 64)])
+@pytest.mark.parametrize("act", [0, 1, 2])
+def test_winograd_shapes(hip, orc, IC, H, W, OC, act):
+    say(f"winograd {IC}->{OC} @{H}x{W} act{act}")
+    rng = np.random.default_rng(IC + H * 5 + W * 7 + OC + act)
+    x, w, b = conv_inputs(rng, IC, H, W, OC, 3)
+    out, dt, yt, _ = hip_winograd(hip, x, w, b, act)
+    y = host(out)
+    assert normwise(y, orc.conv2d_f64(x, w, b, 1, 1, act)) < TOL
+    TW, TH = (W + 3) // 4, (H + 3) // 4
+    out_ref = orc.wg4_output(host(yt), b, TW, TH, H, W, act)
+    if act == 2:
+        assert rel1(y, out_ref) < 1e-6
+    else:
+        assert np.array_equal(y, out_ref), "output transform must be bit-exact"
+    # op 10 on a pre-padded frame == op 15 with the pad fused
+    out2, dt2, _, _ = hip_winograd(hip, x, w, b, act, prepadded=True)
+    assert np.array_equal(host(dt2), host(dt))
+    assert np.array_equal(host(out2), y)
+
+
+# ---------------------------------------------------------------- im2col convs
+IM2COL_CONFIGS = [  # IC, IH, IW, OC, K, S, P
+    (48, 401, 401, 24, 2, 1, 0),    # stem2a-like k2: input padded right/bottom to 401
+    (256, 100, 100, 256, 3, 2, 1),
+    (256, 50, 50, 256, 3, 2, 1),
+    (3, 800, 800, 32, 3, 2, 1),
+]
+
+
+@pytest.mark.parametrize("IC,IH,IW,OC,K,S,P", IM2COL_CONFIGS)
+@pytest.mark.parametrize("act", [0, 1, 2])
+def test_conv_im2col_config3(hip, orc, IC, IH, IW, OC, K, S, P, act):
+    say(f"im2col conv k{K}s{S}p{P} {IC}->{OC} @{IH}x{IW} act{act} (config 3)")
+    rng = np.random.default_rng(SEED + 3 + IC + IH + act)
+    x, w, b = conv_inputs(rng, IC, IH, IW, OC, K)
+    y = host(hip_conv_im2col(hip, x, w, b, K, S, P, act))
+    e = normwise(y, orc.conv2d_ref(x, w, b, S, P, act))
+    say(f"  normwise {e:.2e}")
+    assert e < TOL
+
+
+@pytest.mark.parametrize("IC,IH,IW,OC,K,S,P", [(1, 1, 1, 1, 1, 1, 0), (2, 5, 3, 3, 2, 1, 0), (7, 9, 8, 5, 3, 2, 1),
+                                               (16, 33, 31, 70, 3, 2, 1), (4, 6, 6, 9, 5, 1, 2), (3, 2, 2, 4, 3, 1, 1)])
+def test_conv_im2col_shapes(hip, orc, IC, IH, IW, OC, K, S, P):
+    say(f"im2col conv edge k{K}s{S}p{P} {IC}->{OC} @{IH}x{IW}")
+    rng = np.random.default_rng(IC + IH + IW + OC + K)
+    x, w, b = conv_inputs(rng, IC, IH, IW, OC, K)
+    y = host(hip_conv_im2col(hip, x, w, b, K, S, P, 1))
+    assert normwise(y, orc.conv2d_f64(x, w, b, S, P, 1)) < TOL
+
+
+@pytest.mark.parametrize("IC,IH,IW,K,S,P", [(48, 401, 401, 2, 1, 0), (256, 100, 100, 3, 2, 1), (3, 800, 800, 3, 2, 1),
+                                            (5, 7, 9, 3, 1, 1), (16, 10, 10, 1, 1, 0), (2, 3, 3, 3, 2, 1)])
+def test_im2col_ggml_layout(hip, orc, IC, IH, IW, K, S, P):
+    say(f"im2col ggml layout k{K}s{S}p{P} IC{IC} @{IH}x{IW}")
+    rng = np.random.default_rng(IC + IH + K)
+    x = rng.random((IC, IH, IW)).astype(np.float32)
+    OH, OW = (IH + 2 * P - K) // S + 1, (IW + 2 * P - K) // S + 1
+    d = torch.empty((OH * OW, IC * K * K), device="cuda")
+    assert hip.im2col_f32(dev(x), d, IW, IH, OW, OH, K, K, IC, 1, IH * IW, IC * IH * IW, S, S, P, P, 1, 1) == 1
+    assert np.array_equal(host(d), orc.im2col(x, K, S, P, OH, OW))
+
+
+def test_conv_golden_fixtures_on_gpu(hip, orc):
+    import glob
+    for path in sorted(glob.glob(os.path.join(GOLD, "conv_*.npz"))):
+        f = np.load(path)
+        S, P, act = (int(v) for v in f["meta"])
+        x, w, b = f["x"], f["w"], f["b"]
+        K = w.shape[2]
+        say(f"fixture {os.path.basename(path)}")
+        if K == 1:
+            y = host(hip_conv1x1(hip, x, w, b, act)[0])
+        elif K == 3 and S == 1 and P == 1:
+            y = host(hip_winograd(hip, x, w, b, act)[0])
+        else:
+            y = host(hip_conv_im2col(hip, x, w, b, K, S, P, act))
+        assert normwise(y, f["y"]) < TOL, path
+
+
+# ---------------------------------------------------------------- bias + act
+@pytest.mark.parametrize("shape", [(256, 100, 100), (7, 5, 3), (3, 1, 1)])
+def test_bias_act(hip, orc, shape):
+    rng = np.random.default_rng(sum(shape))
+    x = rng.standard_normal(shape).astype(np.float32)
+    b = rng.standard_normal(shape[0]).astype(np.float32)
+    for act in (0, 1, 2):
+        out = torch.empty(shape, device="cuda")
+        hip.run_checked(hip.OP_BIASACT, out, [dev(x), dev(b)], act)
+        y, ref = host(out), orc.bias_act(x, b, act)
+        if act == 2:
+            assert rel1(y, ref) < 1e-6
+        else:
+            assert np.array_equal(y, ref)
+
+
+# ---------------------------------------------------------------- MSDeformAttn
+def msdef_config4(rng, nq=300):
+    """Config 4: values N(0,1); ref cx,cy U(0,1), w,h U(0.05,1); a normalised
+    displacement d ~ N(0, 0.05) per sample, off = d*8/wh so loc = ref + d,
+    then loc clamped to [-0.1, 1.1] (partly and fully out-of-bounds samples);
+    attention logits N(0,1)."""
+    val = rng.standard_normal((13125, 256)).astype(np.float32)
+    ref = np.concatenate([rng.random((nq, 2)), rng.uniform(0.05, 1.0, (nq, 2))], 1).astype(np.float32)
+    d = rng.normal(0.0, 0.05, (nq, 8, 3, 4, 2))
+    loc = np.clip(ref[:, None, None, None, :2] + d, -0.1, 1.1)
+    off = ((loc - ref[:, None, None, None, :2]) * 8.0 / ref[:, None, None, None, 2:]).astype(np.float32)
+    awr = rng.standard_normal((nq, 96)).astype(np.float32)
+    return val, off.reshape(nq, 192), awr, ref
+
+
+def hip_msdeform(hip, val, off, awr, ref):
+    out = torch.empty((ref.shape[0], 256), device="cuda")
+    hip.run_checked(hip.OP_MSDEF, out, [dev(val), dev(off), dev(awr), dev(ref)])
+    return host(out)
+
+
+def test_msdeform_config4(hip, orc):
+    say("msdeform 300q x 8h x 3lvl x 4pt (config 4)")
+    val, off, awr, ref = msdef_config4(np.random.default_rng(SEED + 4))
+    y = hip_msdeform(hip, val, off, awr, ref)
+    oref = orc.msdeform(val, off, awr, ref)
+    e = normwise(y, oref)
+    say(f"  normwise {e:.2e}, bit-exact fraction {np.mean(y == oref):.3f}")
+    assert e < TOL
+
+
+def test_msdeform_fixture_and_special_cases(hip, orc):
+    f = np.load(os.path.join(GOLD, "msdef_nq7.npz"))
+    val = msdef_value_map(int(f["val_salt"]))
+    assert normwise(hip_msdeform(hip, val, f["off"], f["awr"], f["ref"]), f["y"]) < TOL
+    # all samples outside -> exactly 0
+    far = np.tile(np.array([[5.0, 5.0, 0.5, 0.5]], np.float32), (3, 1))
+    assert not hip_msdeform(hip, val, np.zeros((3, 192), np.float32), np.zeros((3, 96), np.float32), far).any()
+    # texel-centre copy
+    r = np.array([[37.5 / 100, 12.5 / 100, 0.3, 0.3]], np.float32)
+    lg = np.tile(np.array([0] + [-1e4] * 11, np.float32), 8)[None]
+    y = hip_msdeform(hip, val, np.zeros((1, 192), np.float32), lg, r)
+    assert np.array_equal(y[0], val[12 * 100 + 37])
+    # odd query counts
+    rng = np.random.default_rng(3)
+    for nq in (1, 17):
+        v2, o2, a2, r2 = msdef_config4(rng, nq)
+        assert normwise(hip_msdeform(hip, v2, o2, a2, r2), orc.msdeform(v2, o2, a2, r2)) < TOL
+
+
+# ---------------------------------------------------------------- mask box / top-k
+def test_mask_box(hip, orc):
+    rng = np.random.default_rng(21)
+    ml = rng.standard_normal((300, 40000)).astype(np.float32) - 2.5  # sparse positives
+    ml[0] = -1.0               # empty mask
+    ml[1] = 1.0                # full mask
+    ml[2] = -1.0
+    ml[2, 199 * 200 + 199] = 0.5  # single corner pixel
+    out = torch.empty((300, 4), device="cuda")
+    hip.run_checked(hip.OP_MASKBOX, out, [dev(ml)])
+    y, ref = host(out), orc.mask_box(ml)
+    assert rel1(y, ref) < 1e-6
+
+
+def test_topk(hip, orc):
+    rng = np.random.default_rng(22)
+    lg = rng.standard_normal((13125, 25)).astype(np.float32)
+    lg[10:20] = 9.0          # ties -> lower index first
+    lg[7000, 3] = 9.0
+    lg[40] = -0.0            # -0 and +0 compare equal
+    lg[41] = 0.0
+    out = torch.empty((300,), dtype=torch.int32, device="cuda")
+    hip.run_checked(hip.OP_TOPK, out, [dev(lg)])
+    assert np.array_equal(host(out), orc.topk(lg, 300))
+    # all equal -> 0..299
+    eq = np.zeros((13125, 25), np.float32)
+    hip.run_checked(hip.OP_TOPK, out, [dev(eq)])
+    assert np.array_equal(host(out), np.arange(300, dtype=np.int32))
+    small = rng.standard_normal((50, 3)).astype(np.float32)
+    o2 = torch.empty((50,), dtype=torch.int32, device="cuda")
+    hip.run_checked(hip.OP_TOPK, o2, [dev(small)])
+    assert np.array_equal(host(o2), orc.topk(small, 50))
+
+
+# ---------------------------------------------------------------- graph capture
+def test_ops_replay_under_graph_capture(hip):
+    """Every op is capture-safe: a captured sequence replays to the eager
+    result, replay after replay, with eager work in between."""
+    say("graph capture of winograd + 1x1 + msdeform")
+    rng = np.random.default_rng(23)
+    x, w, b = conv_inputs(rng, 64, 50, 50, 64, 3)
+    _, wg4 = hip.repack_conv(w)
+    w1 = (rng.standard_normal((32, 64, 1, 1)) / 8).astype(np.float32)
+    wr1, _ = hip.repack_conv(w1)
+    xt, wgt, bt, w1t = dev(x), dev(wg4), dev(b), dev(wr1)
+    b1 = dev(rng.uniform(-0.1, 0.1, 32).astype(np.float32))
+    T = 13 * 13
+    dt = torch.empty((36, 64, T), device="cuda")
+    yt = torch.empty((36, 64, T), device="cuda")
+    mid = torch.empty((64, 50, 50), device="cuda")
+    out = torch.empty((32, 50, 50), device="cuda")
+    val, off, awr, ref = msdef_config4(rng, 300)
+    vt, ot, at, rt = dev(val), dev(off), dev(awr), dev(ref)
+    ms = torch.empty((300, 256), device="cuda")
+
+    def seq():
+        s = torch.cuda.current_stream().cuda_stream
+        hip.run_checked(hip.OP_WG4_INPUT_PAD, dt, [xt], T, 13, stream=s)
+        hip.run_checked(hip.OP_WG4_MADD, yt, [dt, wgt], stream=s)
+        hip.run_checked(hip.OP_WG4_OUTPUT, mid, [yt, bt], 2, 13, stream=s)
+        hip.run_checked(hip.OP_CONV1X1_BA, out, [mid, w1t, b1], 1, stream=s)
+        hip.run_checked(hip.OP_MSDEF, ms, [vt, ot, at, rt], stream=s)
+
+    seq()
+    eager_out, eager_ms = host(out).copy(), host(ms).copy()
+    g = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(g, stream=side):
+            seq()
+    torch.cuda.current_stream().wait_stream(side)
+    for i in range(3):
+        out.zero_()
+        ms.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(host(out), eager_out), i
+        assert np.array_equal(host(ms), eager_ms), i
+        junk = torch.randn(1000, device="cuda").sum()  # eager work between replays
+        torch.cuda.synchronize()
+        del junk
