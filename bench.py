@@ -54,6 +54,20 @@ def time_nodes(suite, stream, reps):
     return out
 
 
+def measured_traffic(node):
+    """HBM bytes per launch of `node` (FETCH_SIZE + WRITE_SIZE, copy-calibrated)
+    from the committed rocprofv3 summary, or (None, None) if not profiled."""
+    path = os.path.join(ROOT, "profiles", "conv_suite_traffic.json")
+    try:
+        with open(path) as f:
+            rec = json.load(f)["nodes"].get(node)
+    except (OSError, ValueError, KeyError):
+        return None, None
+    if not rec:
+        return None, None
+    return rec["bytes"], "profiles/conv_suite_traffic.json (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE)"
+
+
 def cpu_baseline(budget_s):
     """Suite passes through the oracle's reference CPU path until budget_s."""
     import numpy as np
@@ -97,6 +111,8 @@ def main():
     ap.add_argument("--kernel-reps", type=int, default=20)
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU baseline work")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--calib-copy-mib", type=int, default=0,
+                    help="also run a plain copy of this many MiB (PMC byte-counter calibration)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -144,6 +160,17 @@ def main():
         kt = time_nodes(suite, stream, args.kernel_reps)
     torch.cuda.synchronize()
 
+    if args.calib_copy_mib > 0:
+        # a plain elementwise copy of known size: reads and writes exactly
+        # calib_copy_mib MiB, the scale for HBM byte counters
+        n = args.calib_copy_mib * (1 << 20) // 4
+        a = torch.ones(n, device="cuda")
+        b = torch.empty_like(a)
+        for _ in range(3):
+            torch.mul(a, 1.0, out=b)
+        torch.cuda.synchronize()
+        del a, b
+
     kernels = {}
     gemm_flops = gemm_us = 0.0
     dominant = None
@@ -166,6 +193,7 @@ def main():
 
     dom_us = kt[dominant.name]
     dom_tf = dominant.flops / (dom_us * 1e-6) / 1e12
+    traffic, traffic_src = measured_traffic(dominant.name)
     roofline = {
         "bound": "mfma",
         "kernel": dominant.name,
@@ -173,7 +201,9 @@ def main():
         "peak": PEAK_FP32_MFMA_TFLOPS,
         "unit": "TFLOP/s",
         "frac": round(dom_tf / PEAK_FP32_MFMA_TFLOPS, 4),
-        "traffic": None,
+        "traffic": traffic,
+        "traffic_source": traffic_src,
+        "algorithmic_bytes": dominant.bytes,
         "flops_per_launch": dominant.flops,
         "us_per_launch": round(dom_us, 2),
     }

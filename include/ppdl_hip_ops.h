@@ -104,9 +104,23 @@ PPDL_HIP_API int ppdl_hip_supports(const int32_t op_params[16], const ppdl_tview
  *  16 CONV_IM2COL src: x ne(IW,IH,IC), wr ne(OC,IC,K*K), bias ne(OC);
  *               params[14] = K | S<<8 | P<<16 | act<<24; dst ne(OW,OH,OC),
  *               OW = (IW+2P-K)/S+1.
+ *
+ * Split-K workspace (ops 3, 12, 14, 16): one optional extra src after the
+ * op's own (src[3] for 3/14/16, src[2] for 12), a 16-byte aligned contiguous
+ * buffer of ppdl_hip_workspace_bytes() bytes; its contents are scratch (no
+ * initialisation needed).  Without it, or when it is smaller, the GEMM runs
+ * with fewer or no K splits: results differ only by fp32 summation order, and
+ * a given plan always sums in the same order.  Ops sharing one workspace must
+ * not run concurrently.
  */
 PPDL_HIP_API int ppdl_hip_run(const int32_t op_params[16], const ppdl_tview *dst,
                               const ppdl_tview *src, int nsrc, void *stream);
+
+/* Workspace bytes the node's GEMM plan would use (0 = needs none), or -1 if
+ * the node is invalid.  Host-only; no counterpart in the reference, whose
+ * GEMMs run in cuBLAS with the backend's own workspace. */
+PPDL_HIP_API int64_t ppdl_hip_workspace_bytes(const int32_t op_params[16], const ppdl_tview *dst,
+                                              const ppdl_tview *src, int nsrc);
 
 /* F32 im2col in ggml's layout: dst[pix][k], pix = (n*OH + oh)*OW + ow,
  * k = ic*KH*KW + kh*KW + kw, zero where the tap falls outside the input.

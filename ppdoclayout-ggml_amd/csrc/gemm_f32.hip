@@ -8,18 +8,31 @@
 //                             B = dt[p][ic][tile], C = yt[p][oc][tile];
 //   * k2 / k3-s2 conv (16):   At = wr[tap][ic][oc], B = an implicit im2col view
 //                             of the CHW input (no column buffer in HBM).
-// Every operand is k-major, so both global loads and C stores are coalesced
-// along the fastest axis (m for At, n for B and C).
+// Every operand is k-major, so global loads and C stores are contiguous along
+// the fastest axis (m for At, n for B and C).
 //
 // Tiling: a 256-thread block = 4 wave64s owns a BM x BN tile of C; each wave
-// owns WM x WN = (32*TM) x (32*TN) of it as TM*TN 32x32 MFMA accumulators
-// (16 fp32 per lane each).  K advances 16 at a time through a double-buffered
-// LDS stage: the next tile's global loads are in flight while the MFMAs of
-// the current one issue.  Inside a 16-deep k tile, lanes 0-31 supply k rows
-// 0..7 and lanes 32-63 rows 8..15 to the 8 MFMAs (each MFMA contracts 2 k),
-// which keeps every LDS read a row-contiguous 32-float run (no bank conflict
-// with the +4 row pad).  No TF32/bf16 emulation anywhere: the products and
-// the accumulation are IEEE fp32 inside the matrix core.
+// owns (32*TM) x (32*TN) of it as TM*TN 32x32 MFMA accumulators.  K advances
+// BK = 32 at a time through a double-buffered LDS stage fed by a two-deep
+// register prefetch: while the MFMAs of k tile t issue, tile t+1 waits in
+// registers for its LDS slot and tile t+2's global loads are in flight, so a
+// load has two tiles of MFMA work to hide behind.  Inside a k tile, lanes
+// 0-31 feed k rows 0..15 and lanes 32-63 rows 16..31 to the 16 MFMA steps
+// (each MFMA contracts 2 k); all fragments of a tile are read from LDS before
+// its MFMAs issue, so LDS latency overlaps the matrix pipe.
+//
+// Split-K (optional, for long-K shapes with few output tiles): S blocks share
+// one output tile, each contracting a contiguous range of k tiles and storing
+// its fp32 partial tile to a caller-provided workspace; a second small kernel
+// sums the S partials in fixed order s = 0..S-1 and applies bias/act.  The
+// kernel boundary orders the two, so no block waits on or fences for another,
+// and the result does not depend on scheduling.
+//
+// No TF32/bf16 emulation anywhere: products and accumulation are IEEE fp32 in
+// the matrix core; split partials are summed in fp32.
+#include <cstdlib>
+#include <type_traits>
+
 #include "ppdl_internal.h"
 
 namespace ppdl {
@@ -28,7 +41,7 @@ namespace {
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kThreads = 256;
-constexpr int kBK = 16;
+constexpr int kBK = 32;
 
 __device__ __forceinline__ float act_f(float v, int act) {
     if (act == 1) return v > 0.0f ? v : 0.0f;
@@ -45,77 +58,81 @@ __device__ __forceinline__ int xcd_remap(int hw, int n) {
     return xcd * q + (xcd < r ? xcd : r) + slot;
 }
 
-template <int BM, int BN, int WGM, bool IM2COL>
-__global__ __launch_bounds__(kThreads) void k_gemm(GemmArgs g, int tiles_m, int tiles_mn) {
+__device__ __forceinline__ float4 ld4(const float *p) {
+    float4 v;
+    __builtin_memcpy(&v, p, 16);  // dword-aligned dwordx4 load
+    return v;
+}
+
+struct SplitArgs {
+    int splits;  // S (1 = no split)
+    int ktiles_per_split;
+    float *partials;  // S x batch x M x N
+};
+
+// Per-thread staging registers for one k tile.
+template <int EA, int EB4, int EB1>
+struct Stage {
+    float4 a[EA];
+    float4 b4[EB4];
+    float b1[EB1];
+    uint32_t ok1;  // im2col: bit e set when element e is inside the image
+};
+
+// BMODE 0: dense B; BMODE 1: implicit im2col B
+template <int BM, int BN, int WGM, int BMODE, bool SPLIT>
+__global__ __launch_bounds__(kThreads) void k_gemm(GemmArgs g, SplitArgs sp, int tiles_m, int tiles_mn) {
     constexpr int WGN = 4 / WGM;
     constexpr int WM = BM / WGM, WN = BN / WGN;
     constexpr int TM = WM / 32, TN = WN / 32;
     constexpr int PA = BM + 4, PB = BN + 4;
-    constexpr int EA = kBK * BM / kThreads, EB = kBK * BN / kThreads;
-    constexpr int RA = kThreads / BM, RB = kThreads / BN;
-    static_assert(TM >= 1 && TN >= 1 && EA >= 1 && EB >= 1, "bad tile");
+    // A: float4 along m; threads per k row = BM/4
+    constexpr int TA = BM / 4, RA = kThreads / TA, EA = kBK / RA;
+    // B dense: float4 along n; B im2col: one column per thread
+    constexpr int TB4 = BN / 4, RB4 = kThreads / TB4, EB4 = BMODE == 0 ? kBK / RB4 : 1;
+    constexpr int RB1 = kThreads / BN, EB1 = BMODE == 1 ? kBK / RB1 : 1;
+    constexpr int KH = kBK / 2;  // MFMA k-steps per tile
+    static_assert(TM >= 1 && TN >= 1 && EA >= 1 && EB4 >= 1 && EB1 >= 1, "bad tile");
     static_assert(WM % 32 == 0 && WN % 32 == 0, "wave tile must be 32-aligned");
+    using St = Stage<EA, EB4, EB1>;
 
-    __shared__ float As[2][kBK][PA];
-    __shared__ float Bs[2][kBK][PB];
+    __shared__ __attribute__((aligned(16))) float As[2][kBK][PA];
+    __shared__ __attribute__((aligned(16))) float Bs[2][kBK][PB];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int logical = xcd_remap(blockIdx.x, gridDim.x);
-    const int bz = logical / tiles_mn;
-    const int t = logical - bz * tiles_mn;
+    const int S = SPLIT ? sp.splits : 1;
+    const int split = SPLIT ? logical % S : 0;
+    const int tile_id = SPLIT ? logical / S : logical;
+    const int bz = tile_id / tiles_mn;
+    const int t = tile_id - bz * tiles_mn;
     const int tm = t % tiles_m, tn = t / tiles_m;
     const int m0 = tm * BM, n0 = tn * BN;
+    const int M = g.M, N = g.N, K = g.K;
+
+    const int nk_total = (K + kBK - 1) / kBK;
+    const int kt0 = SPLIT ? split * sp.ktiles_per_split : 0;
+    const int kt1 = SPLIT ? min(nk_total, kt0 + sp.ktiles_per_split) : nk_total;
+    const int nk = kt1 - kt0;
 
     const float *__restrict__ A = g.A + (int64_t)bz * g.sA;
     const float *__restrict__ B = g.B + (int64_t)bz * g.sB;
-    float *__restrict__ C = g.C + (int64_t)bz * g.sC;
-    const int M = g.M, N = g.N, K = g.K;
 
-    // loader coordinates: each thread owns one m column of the A tile and one
-    // n column of the B tile, and walks k rows RA / RB apart
-    const int am = tid % BM, ak = tid / BM;
-    const int bn = tid % BN, bk = tid / BN;
-    const int gm = m0 + am, gn = n0 + bn;
-    const bool am_ok = gm < M, bn_ok = gn < N;
+    // ---- loader state ----
+    const int am = (tid % TA) * 4, ak = tid / TA;
+    const int gm = m0 + am;
+    const int bn4 = (tid % TB4) * 4, bk4 = tid / TB4;  // dense B
+    const int gn4 = n0 + bn4;
+    const int bn1 = tid % BN, bk1 = tid / BN;  // im2col B
+    const int gn1 = n0 + bn1;
+    const bool bn_ok = gn1 < N;
     int iy0 = 0, ix0 = 0;
-    if (IM2COL) {
-        const int oy = gn / g.OW, ox = gn - oy * g.OW;
+    if (BMODE == 1) {
+        const int oy = gn1 / g.OW, ox = gn1 - oy * g.OW;
         iy0 = oy * g.S - g.P;
         ix0 = ox * g.S - g.P;
     }
     const int64_t plane = (int64_t)g.IH * g.IW;
-
-    float ra[EA], rb[EB];
-    auto load = [&](int k0) {
-#pragma unroll
-        for (int e = 0; e < EA; e++) {
-            const int k = k0 + ak + e * RA;
-            ra[e] = (am_ok && k < K) ? A[(int64_t)k * g.lda + gm] : 0.0f;
-        }
-#pragma unroll
-        for (int e = 0; e < EB; e++) {
-            const int k = k0 + bk + e * RB;
-            float v = 0.0f;
-            if (bn_ok && k < K) {
-                if (IM2COL) {
-                    const int tap = k / g.IC, ic = k - tap * g.IC;
-                    const int kh = tap / g.KW, kw = tap - kh * g.KW;
-                    const int iy = iy0 + kh, ix = ix0 + kw;
-                    if (iy >= 0 && iy < g.IH && ix >= 0 && ix < g.IW)
-                        v = B[ic * plane + (int64_t)iy * g.IW + ix];
-                } else {
-                    v = B[(int64_t)k * g.ldb + gn];
-                }
-            }
-            rb[e] = v;
-        }
-    };
-    auto store = [&](int buf) {
-#pragma unroll
-        for (int e = 0; e < EA; e++) As[buf][ak + e * RA][am] = ra[e];
-#pragma unroll
-        for (int e = 0; e < EB; e++) Bs[buf][bk + e * RB][bn] = rb[e];
-    };
 
     f32x16 acc[TM][TN];
 #pragma unroll
@@ -126,36 +143,171 @@ __global__ __launch_bounds__(kThreads) void k_gemm(GemmArgs g, int tiles_m, int 
             for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
 
     const int wm0 = (wave % WGM) * WM, wn0 = (wave / WGM) * WN;
-    const int l32 = lane & 31, lk = (lane >> 5) * (kBK / 2);
-    const int nk = (K + kBK - 1) / kBK;
+    const int l32 = lane & 31, lk = (lane >> 5) * KH;
 
-    load(0);
-    store(0);
-    __syncthreads();
-    for (int kt = 0; kt < nk; kt++) {
-        const int cur = kt & 1;
-        if (kt + 1 < nk) load((kt + 1) * kBK);
+    auto compute = [&](int buf) {
+        float a[KH][TM], b[KH][TN];
 #pragma unroll
-        for (int kk = 0; kk < kBK / 2; kk++) {
-            float a[TM], b[TN];
+        for (int kk = 0; kk < KH; kk++) {
 #pragma unroll
-            for (int i = 0; i < TM; i++) a[i] = As[cur][lk + kk][wm0 + i * 32 + l32];
+            for (int i = 0; i < TM; i++) a[kk][i] = As[buf][lk + kk][wm0 + i * 32 + l32];
 #pragma unroll
-            for (int j = 0; j < TN; j++) b[j] = Bs[cur][lk + kk][wn0 + j * 32 + l32];
+            for (int j = 0; j < TN; j++) b[kk][j] = Bs[buf][lk + kk][wn0 + j * 32 + l32];
+        }
+#pragma unroll
+        for (int kk = 0; kk < KH; kk++)
 #pragma unroll
             for (int i = 0; i < TM; i++)
 #pragma unroll
                 for (int j = 0; j < TN; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], b[j], acc[i][j], 0, 0, 0);
-        }
-        if (kt + 1 < nk) store(cur ^ 1);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[kk][i], b[kk][j], acc[i][j], 0, 0, 0);
+    };
+
+    // The loads only issue (clamped, always-valid addresses); every mask is
+    // applied when the stage is written to LDS.  That keeps a fixed number of
+    // loads per stage with no use of their results before the store, so the
+    // compiler waits for one stage while the next stays in flight.  The
+    // edge/interior choice is made once per block (EDGE): interior tiles load
+    // float4 rows, tiles crossing M or N load clamped scalars.
+    auto body = [&](auto edge_tag) {
+        constexpr bool EDGE = decltype(edge_tag)::value;
+        auto load = [&](St &r, int kt) {
+            const int k0 = kt * kBK;
+#pragma unroll
+            for (int e = 0; e < EA; e++) {
+                const int k = min(k0 + ak + e * RA, K - 1);
+                const float *row = A + (int64_t)k * g.lda;
+                if (!EDGE) {
+                    r.a[e] = ld4(row + gm);
+                } else {
+                    r.a[e].x = row[min(gm + 0, M - 1)];
+                    r.a[e].y = row[min(gm + 1, M - 1)];
+                    r.a[e].z = row[min(gm + 2, M - 1)];
+                    r.a[e].w = row[min(gm + 3, M - 1)];
+                }
+            }
+            if (BMODE == 0) {
+#pragma unroll
+                for (int e = 0; e < EB4; e++) {
+                    const int k = min(k0 + bk4 + e * RB4, K - 1);
+                    const float *row = B + (int64_t)k * g.ldb;
+                    if (!EDGE) {
+                        r.b4[e] = ld4(row + gn4);
+                    } else {
+                        r.b4[e].x = row[min(gn4 + 0, N - 1)];
+                        r.b4[e].y = row[min(gn4 + 1, N - 1)];
+                        r.b4[e].z = row[min(gn4 + 2, N - 1)];
+                        r.b4[e].w = row[min(gn4 + 3, N - 1)];
+                    }
+                }
+            } else {
+                // k = (kh*KW + kw)*IC + ic: decompose the first row once, then
+                // step ic by RB1 with carries into kw and kh
+                int k = k0 + bk1;
+                int tap = k / g.IC;
+                int ic = k - tap * g.IC;
+                int kh = tap / g.KW;
+                int kw = tap - kh * g.KW;
+                uint32_t okm = 0;
+#pragma unroll
+                for (int e = 0; e < EB1; e++) {
+                    const int iy = iy0 + kh, ix = ix0 + kw;
+                    const bool ok = bn_ok && k < K && iy >= 0 && iy < g.IH && ix >= 0 && ix < g.IW;
+                    r.b1[e] = B[ok ? ic * plane + (int64_t)iy * g.IW + ix : 0];
+                    okm |= (ok ? 1u : 0u) << e;
+                    k += RB1;
+                    ic += RB1;
+                    while (ic >= g.IC) {
+                        ic -= g.IC;
+                        if (++kw == g.KW) {
+                            kw = 0;
+                            ++kh;
+                        }
+                    }
+                }
+                r.ok1 = okm;
+            }
+        };
+        auto store = [&](const St &r, int buf, int kt) {
+            const int k0 = kt * kBK;
+#pragma unroll
+            for (int e = 0; e < EA; e++) {
+                float4 v = r.a[e];
+                const bool kin = k0 + ak + e * RA < K;
+                v.x = (kin && (!EDGE || gm + 0 < M)) ? v.x : 0.0f;
+                v.y = (kin && (!EDGE || gm + 1 < M)) ? v.y : 0.0f;
+                v.z = (kin && (!EDGE || gm + 2 < M)) ? v.z : 0.0f;
+                v.w = (kin && (!EDGE || gm + 3 < M)) ? v.w : 0.0f;
+                *reinterpret_cast<float4 *>(&As[buf][ak + e * RA][am]) = v;
+            }
+            if (BMODE == 0) {
+#pragma unroll
+                for (int e = 0; e < EB4; e++) {
+                    float4 v = r.b4[e];
+                    const bool kin = k0 + bk4 + e * RB4 < K;
+                    v.x = (kin && (!EDGE || gn4 + 0 < N)) ? v.x : 0.0f;
+                    v.y = (kin && (!EDGE || gn4 + 1 < N)) ? v.y : 0.0f;
+                    v.z = (kin && (!EDGE || gn4 + 2 < N)) ? v.z : 0.0f;
+                    v.w = (kin && (!EDGE || gn4 + 3 < N)) ? v.w : 0.0f;
+                    *reinterpret_cast<float4 *>(&Bs[buf][bk4 + e * RB4][bn4]) = v;
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < EB1; e++) Bs[buf][bk1 + e * RB1][bn1] = ((r.ok1 >> e) & 1u) ? r.b1[e] : 0.0f;
+            }
+        };
+
+        // two-deep pipeline: r0/r1 alternate as the staging registers of even
+        // / odd k tiles, LDS buffer 0/1 likewise.  Prefetches past the last
+        // tile reload the last tile (never stored): keeping every load
+        // unconditional keeps the in-flight count static.
+        if (nk <= 0) return;  // an empty split range contributes zeros
+        const int klast = kt1 - 1;
+        St r0, r1;
+        load(r0, kt0);
+        store(r0, 0, kt0);
+        load(r1, min(kt0 + 1, klast));
         __syncthreads();
+        for (int it = 0; it < nk; it += 2) {
+            load(r0, min(kt0 + it + 2, klast));
+            compute(0);
+            if (it + 1 < nk) store(r1, 1, kt0 + it + 1);
+            __syncthreads();
+            if (it + 1 >= nk) break;
+            load(r1, min(kt0 + it + 3, klast));
+            compute(1);
+            if (it + 2 < nk) store(r0, 0, kt0 + it + 2);
+            __syncthreads();
+        }
+    };
+    if (m0 + BM > M || n0 + BN > N)
+        body(std::true_type{});
+    else
+        body(std::false_type{});
+
+    // 32x32 accumulator layout: lane owns column (lane & 31) and rows
+    // 8*(r/4) + 4*(lane/32) + r%4 of register r
+    if (SPLIT) {
+        float *__restrict__ P = sp.partials + ((int64_t)split * g.batch + bz) * M * N;
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+            const int n = n0 + wn0 + j * 32 + l32;
+            if (n < N) {
+#pragma unroll
+                for (int i = 0; i < TM; i++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++) {
+                        const int m = m0 + wm0 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                        if (m < M) P[(int64_t)m * N + n] = acc[i][j][r];
+                    }
+            }
+        }
+        return;
     }
 
-    // epilogue: 32x32 accumulator layout — lane owns column (lane & 31) and
-    // rows 8*(r/4) + 4*(lane/32) + r%4 of register r
     const float *__restrict__ bias = g.bias;
     const int act = g.act;
+    float *__restrict__ C = g.C + (int64_t)bz * g.sC;
 #pragma unroll
     for (int j = 0; j < TN; j++) {
         const int n = n0 + wn0 + j * 32 + l32;
@@ -176,67 +328,160 @@ __global__ __launch_bounds__(kThreads) void k_gemm(GemmArgs g, int tiles_m, int 
     }
 }
 
+// Split-K fix-up: C = act(sum_{s=0..S-1} P[s] + bias), s ascending.  C is
+// contiguous per batch plane (ldc == N, sC == M*N) for every op that splits.
+template <int VEC>
+__global__ __launch_bounds__(256) void k_splitk_reduce(const float *__restrict__ P, int S, int64_t total,
+                                                       int64_t MN, int N, int M, const float *__restrict__ bias,
+                                                       int act, float *__restrict__ C) {
+    const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * VEC;
+    if (i >= total) return;
+    const int m = (int)((i % MN) / N);
+    const float b = bias ? bias[m] : 0.0f;
+    if (VEC == 4) {
+        float4 v = *reinterpret_cast<const float4 *>(P + i);
+        for (int s = 1; s < S; s++) {
+            const float4 u = *reinterpret_cast<const float4 *>(P + s * total + i);
+            v.x += u.x;
+            v.y += u.y;
+            v.z += u.z;
+            v.w += u.w;
+        }
+        v.x = act_f(v.x + b, act);
+        v.y = act_f(v.y + b, act);
+        v.z = act_f(v.z + b, act);
+        v.w = act_f(v.w + b, act);
+        *reinterpret_cast<float4 *>(C + i) = v;
+    } else {
+        float v = P[i];
+        for (int s = 1; s < S; s++) v += P[s * total + i];
+        C[i] = act_f(v + b, act);
+    }
+}
+
 struct TileCfg {
     int bm, bn, wgm;
 };
-// Candidate block shapes (BM, BN, waves along M).  Wave tiles range from
-// 64x64 (4 accumulators) down to 32x32.
+// Block shapes (BM, BN, waves along M); wave tiles 64x64 .. 32x32.
 constexpr TileCfg kCfgs[] = {
-    {128, 128, 2},  // wave 64x64
-    {64, 128, 2},   // wave 32x64
-    {128, 64, 2},   // wave 64x32
-    {64, 64, 2},    // wave 32x32
-    {32, 256, 1},   // wave 32x64
-    {32, 128, 1},   // wave 32x32
+    {128, 128, 2},  // 0: wave 64x64
+    {64, 128, 2},   // 1: wave 32x64
+    {128, 64, 2},   // 2: wave 64x32
+    {64, 64, 2},    // 3: wave 32x32
+    {32, 256, 1},   // 4: wave 32x64
+    {32, 128, 1},   // 5: wave 32x32
 };
-constexpr int kNumSimd = 256 * 4;  // MI355X: 256 CUs x 4 SIMDs
+constexpr int kNumCfg = sizeof(kCfgs) / sizeof(kCfgs[0]);
+constexpr int kSplitChoices[] = {1, 2, 3, 4, 6, 8, 12, 16};
 
-// Pick the block shape that minimises the MFMA time of the busiest SIMD:
-// rounds(wave tiles / SIMDs) x MFMAs per wave tile, plus the padding waste of
-// partial tiles.  Ties go to the larger tile (less LDS and L2 traffic).
-int pick_cfg(int M, int N, int batch) {
-    int best = 0;
-    double best_cost = 1e300;
-    for (int c = 0; c < (int)(sizeof(kCfgs) / sizeof(kCfgs[0])); c++) {
-        const TileCfg &t = kCfgs[c];
-        const int64_t tiles = (int64_t)((M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn) * batch;
-        const int64_t waves = tiles * 4;
-        const int64_t rounds = (waves + kNumSimd - 1) / kNumSimd;
-        const int tm = t.bm / t.wgm / 32, tn = t.bn / (4 / t.wgm) / 32;
-        const double cost = (double)rounds * tm * tn * (1.0 + 0.02 * (4.0 / (tm * tn)));
-        if (cost < best_cost - 1e-9) {
-            best_cost = cost;
-            best = c;
-        }
-    }
-    return best;
+int64_t tiles_of(int c, int M, int N, int batch) {
+    return (int64_t)((M + kCfgs[c].bm - 1) / kCfgs[c].bm) * ((N + kCfgs[c].bn - 1) / kCfgs[c].bn) * batch;
 }
 
-template <int BM, int BN, int WGM, bool IM2COL>
-hipError_t launch(const GemmArgs &g, hipStream_t s) {
+// Plan from a sweep of every (block shape, splits) pair on the network's
+// GEMM shapes (1x1 convs 64..2048 x 625..40000 x 64..3328, the F(4,3)
+// planes, the k2/k3-s2 im2col convs).  64x64 blocks (four resident per CU)
+// won or tied nearly everywhere; 32-row blocks when M <= 32.  Splitting K
+// paid only when the output had too few tiles to occupy the chip: the best
+// S kept about 1000 blocks in flight with at least 6 k tiles per split.
+GemmPlan plan_auto(int M, int N, int K, int batch) {
+    GemmPlan p{M <= 32 ? 5 : 3, 1};
+    const int nk = (K + kBK - 1) / kBK;
+    const int64_t tiles = tiles_of(p.cfg, M, N, batch);
+    int64_t want = 1000 / (tiles > 0 ? tiles : 1);
+    const int64_t cap = nk / 6;
+    if (want > cap) want = cap;
+    for (int S : kSplitChoices)
+        if (S <= want) p.splits = S;
+    return p;
+}
+
+// PPDL_GEMM_TILE="cfg,splits" pins the plan (tile-shape tuning sweeps only).
+int env_override(int *cfg, int *splits) {
+    const char *e = getenv("PPDL_GEMM_TILE");
+    if (!e || !*e) return 0;
+    char *end = nullptr;
+    const int oc = (int)strtol(e, &end, 10);
+    const int os = (end && *end == ',') ? (int)strtol(end + 1, nullptr, 10) : 1;
+    if (oc < 0 || oc >= kNumCfg) return 0;
+    *cfg = oc;
+    *splits = os < 1 ? 1 : os;
+    return 1;
+}
+
+template <int BM, int BN, int WGM, int BMODE>
+hipError_t launch(const GemmArgs &g, int S, const GemmWorkspace &ws, hipStream_t s) {
     const int tiles_m = (g.M + BM - 1) / BM, tiles_n = (g.N + BN - 1) / BN;
-    const int64_t total = (int64_t)tiles_m * tiles_n * g.batch;
+    const int64_t tiles = (int64_t)tiles_m * tiles_n * g.batch;
+    const int64_t total = tiles * S;
     if (total <= 0 || total > 0x7fffffff) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((k_gemm<BM, BN, WGM, IM2COL>), dim3((unsigned)total), dim3(kThreads), 0, s,
-                       g, tiles_m, tiles_m * tiles_n);
+    SplitArgs sp{1, 0, nullptr};
+    if (S > 1) {
+        const int nk = (g.K + kBK - 1) / kBK;
+        sp.splits = S;
+        sp.ktiles_per_split = (nk + S - 1) / S;
+        sp.partials = (float *)ws.base;
+        hipLaunchKernelGGL((k_gemm<BM, BN, WGM, BMODE, true>), dim3((unsigned)total), dim3(kThreads), 0, s, g,
+                           sp, tiles_m, tiles_m * tiles_n);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        const int64_t MN = (int64_t)g.M * g.N, n = MN * g.batch;
+        const bool vec = (g.N % 4 == 0) && ((((uintptr_t)g.C) & 15) == 0);
+        if (vec)
+            hipLaunchKernelGGL(k_splitk_reduce<4>, dim3((unsigned)((n / 4 + 255) / 256)), dim3(256), 0, s,
+                               sp.partials, S, n, MN, g.N, g.M, g.bias, g.act, g.C);
+        else
+            hipLaunchKernelGGL(k_splitk_reduce<1>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
+                               sp.partials, S, n, MN, g.N, g.M, g.bias, g.act, g.C);
+    } else {
+        hipLaunchKernelGGL((k_gemm<BM, BN, WGM, BMODE, false>), dim3((unsigned)total), dim3(kThreads), 0, s,
+                           g, sp, tiles_m, tiles_m * tiles_n);
+    }
     return hipGetLastError();
 }
 
-template <bool IM2COL>
-hipError_t dispatch(const GemmArgs &g, hipStream_t s) {
-    switch (pick_cfg(g.M, g.N, g.batch)) {
-        case 0: return launch<128, 128, 2, IM2COL>(g, s);
-        case 1: return launch<64, 128, 2, IM2COL>(g, s);
-        case 2: return launch<128, 64, 2, IM2COL>(g, s);
-        case 3: return launch<64, 64, 2, IM2COL>(g, s);
-        case 4: return launch<32, 256, 1, IM2COL>(g, s);
-        default: return launch<32, 128, 1, IM2COL>(g, s);
+template <int BMODE>
+hipError_t dispatch(const GemmArgs &g, const GemmWorkspace &ws, hipStream_t s) {
+    const GemmPlan p = gemm_plan(g, ws.bytes);
+    switch (p.cfg) {
+        case 0: return launch<128, 128, 2, BMODE>(g, p.splits, ws, s);
+        case 1: return launch<64, 128, 2, BMODE>(g, p.splits, ws, s);
+        case 2: return launch<128, 64, 2, BMODE>(g, p.splits, ws, s);
+        case 3: return launch<64, 64, 2, BMODE>(g, p.splits, ws, s);
+        case 4: return launch<32, 256, 1, BMODE>(g, p.splits, ws, s);
+        default: return launch<32, 128, 1, BMODE>(g, p.splits, ws, s);
     }
 }
 
 }  // namespace
 
-hipError_t gemm_dense(const GemmArgs &g, hipStream_t s) { return dispatch<false>(g, s); }
-hipError_t gemm_im2col(const GemmArgs &g, hipStream_t s) { return dispatch<true>(g, s); }
+int64_t gemm_ws_bytes(int M, int N, int batch, int cfg, int splits) {
+    (void)cfg;
+    if (splits <= 1) return 0;
+    return (int64_t)splits * batch * M * N * 4;
+}
+
+GemmPlan gemm_plan(const GemmArgs &g, int64_t ws_bytes) {
+    GemmPlan best;
+    int oc, os;
+    const int nk = (g.K + kBK - 1) / kBK;
+    if (env_override(&oc, &os)) {
+        best.cfg = oc;
+        best.splits = os < nk ? os : nk;  // at most one split per k tile
+    } else {
+        best = plan_auto(g.M, g.N, g.K, g.batch);
+    }
+    // never plan more splits than the workspace holds
+    while (best.splits > 1 && gemm_ws_bytes(g.M, g.N, g.batch, best.cfg, best.splits) > ws_bytes) best.splits--;
+    return best;
+}
+
+int64_t gemm_ws_bytes_for(const GemmArgs &g) {
+    const GemmPlan p = gemm_plan(g, INT64_MAX);
+    return gemm_ws_bytes(g.M, g.N, g.batch, p.cfg, p.splits);
+}
+
+hipError_t gemm_dense(const GemmArgs &g, const GemmWorkspace &ws, hipStream_t s) { return dispatch<0>(g, ws, s); }
+hipError_t gemm_im2col(const GemmArgs &g, const GemmWorkspace &ws, hipStream_t s) { return dispatch<1>(g, ws, s); }
 
 }  // namespace ppdl

@@ -61,8 +61,22 @@ struct GemmArgs {
     int IC, IH, IW, OW, KW, S, P;
 };
 
-hipError_t gemm_dense(const GemmArgs &g, hipStream_t s);
-hipError_t gemm_im2col(const GemmArgs &g, hipStream_t s);
+// Split-K workspace: fp32 partials, splits x batch x M x N, fully rewritten by
+// every launch that uses it (no initial contents required).
+struct GemmWorkspace {
+    void *base;
+    int64_t bytes;
+};
+struct GemmPlan {
+    int cfg;     // block-shape index
+    int splits;  // split-K factor (1 = none)
+};
+
+GemmPlan gemm_plan(const GemmArgs &g, int64_t ws_bytes);
+int64_t gemm_ws_bytes(int M, int N, int batch, int cfg, int splits);
+int64_t gemm_ws_bytes_for(const GemmArgs &g);  // workspace the unconstrained plan uses
+hipError_t gemm_dense(const GemmArgs &g, const GemmWorkspace &ws, hipStream_t s);
+hipError_t gemm_im2col(const GemmArgs &g, const GemmWorkspace &ws, hipStream_t s);
 
 // ---- Winograd transforms ----
 // pad: 0 when x is already padded (op 10), 1 when the conv's pad is fused.

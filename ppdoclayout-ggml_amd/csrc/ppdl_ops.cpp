@@ -49,6 +49,30 @@ int status_of(hipError_t e) { return e == hipSuccess ? PPDL_OK : PPDL_ELAUNCH; }
 
 constexpr int64_t kMaxI32 = 0x7fffffff;
 
+// Index of the optional split-K workspace src of a GEMM op, or -1.
+int ws_index(int op) {
+    switch (op) {
+        case PPDL_OP_CONV:
+        case PPDL_OP_CONV1X1_BA:
+        case PPDL_OP_CONV_IM2COL: return 3;
+        case PPDL_OP_WG4_MADD: return 2;
+        default: return -1;
+    }
+}
+
+bool ws_valid(const ppdl_tview *t) {
+    if (!t->data || (t->type != PPDL_TYPE_F32 && t->type != PPDL_TYPE_I32) || t->nb[0] != 4) return false;
+    for (int i = 1; i < 4; i++)
+        if (t->ne[i] < 1 || t->nb[i] != t->nb[i - 1] * t->ne[i - 1]) return false;
+    return t->ne[0] >= 1 && aligned16(t->data);
+}
+
+GemmWorkspace ws_of(int op, const ppdl_tview *src, int nsrc) {
+    const int i = ws_index(op);
+    if (i < 0 || nsrc <= i) return GemmWorkspace{nullptr, 0};
+    return GemmWorkspace{src[i].data, nelem(&src[i]) * 4};
+}
+
 // ---- per-op validation (shared by supports() and run()) ----
 // Returns PPDL_OK when the node satisfies the op's contract, PPDL_EINVAL when
 // it does not, PPDL_UNSUPPORTED for an op id this library does not execute.
@@ -69,6 +93,8 @@ int check_conv1x1(const int32_t *p, const ppdl_tview *dst, const ppdl_tview *src
 }
 
 int check_op(const int32_t *p, const ppdl_tview *dst, const ppdl_tview *src, int nsrc) {
+    const int wi = ws_index(p[13]);
+    if (wi >= 0 && nsrc > wi && !ws_valid(&src[wi])) return PPDL_EINVAL;
     switch (p[13]) {
         case PPDL_OP_CONV: {
             const int K = p[14] & 0xFF, pad = (p[14] >> 8) & 0xFF;
@@ -170,7 +196,91 @@ int check_op(const int32_t *p, const ppdl_tview *dst, const ppdl_tview *src, int
     }
 }
 
+// GEMM description of a validated conv/madd node.  Returns false for ops that
+// are not GEMMs.  *im2col selects the implicit-im2col B operand.
+bool gemm_args_of(const int32_t *p, const ppdl_tview *dst, const ppdl_tview *src, GemmArgs *g, bool *im2col) {
+    *g = GemmArgs{};
+    *im2col = false;
+    switch (p[13]) {
+        case PPDL_OP_CONV:
+        case PPDL_OP_CONV1X1_BA: {
+            const ppdl_tview *x = &src[0], *w = &src[1];
+            const bool fused = p[13] == PPDL_OP_CONV1X1_BA;
+            g->A = (const float *)w->data;
+            g->lda = dst->ne[2];
+            g->B = (const float *)x->data;
+            g->ldb = x->ne[0] * x->ne[1];
+            g->C = (float *)dst->data;
+            g->ldc = dst->ne[0] * dst->ne[1];
+            g->bias = fused ? (const float *)src[2].data : nullptr;
+            g->M = (int)dst->ne[2];
+            g->N = (int)(x->ne[0] * x->ne[1]);
+            g->K = (int)x->ne[2];
+            g->batch = 1;
+            g->act = fused ? p[14] : 0;
+            return true;
+        }
+        case PPDL_OP_WG4_MADD: {
+            const int64_t T = src[0].ne[0], IC = src[0].ne[1], OC = src[1].ne[0];
+            g->A = (const float *)src[1].data;
+            g->lda = OC;
+            g->sA = IC * OC;
+            g->B = (const float *)src[0].data;
+            g->ldb = T;
+            g->sB = IC * T;
+            g->C = (float *)dst->data;
+            g->ldc = T;
+            g->sC = OC * T;
+            g->M = (int)OC;
+            g->N = (int)T;
+            g->K = (int)IC;
+            g->batch = 36;
+            return true;
+        }
+        case PPDL_OP_CONV_IM2COL: {
+            const ppdl_tview *x = &src[0];
+            const int K = p[14] & 0xFF, S = (p[14] >> 8) & 0xFF, P = (p[14] >> 16) & 0xFF;
+            g->A = (const float *)src[1].data;
+            g->lda = dst->ne[2];
+            g->B = (const float *)x->data;
+            g->C = (float *)dst->data;
+            g->ldc = dst->ne[0] * dst->ne[1];
+            g->bias = (const float *)src[2].data;
+            g->M = (int)dst->ne[2];
+            g->N = (int)(dst->ne[0] * dst->ne[1]);
+            g->K = (int)(x->ne[2] * K * K);
+            g->batch = 1;
+            g->act = (p[14] >> 24) & 0xFF;
+            g->IC = (int)x->ne[2];
+            g->IH = (int)x->ne[1];
+            g->IW = (int)x->ne[0];
+            g->OW = (int)dst->ne[0];
+            g->KW = K;
+            g->S = S;
+            g->P = P;
+            *im2col = true;
+            return true;
+        }
+        default:
+            return false;
+    }
+}
+
 }  // namespace
+
+extern "C" PPDL_HIP_API int64_t ppdl_hip_workspace_bytes(const int32_t op_params[16], const ppdl_tview *dst,
+                                                         const ppdl_tview *src, int nsrc) {
+    if (!op_params || (uint32_t)op_params[12] != (uint32_t)PPDL_MAGIC || !dst || nsrc < 0 ||
+        (nsrc > 0 && !src))
+        return -1;
+    const int wi = ws_index(op_params[13]);
+    const int n = (wi >= 0 && nsrc > wi) ? wi : nsrc;  // ignore a workspace already attached
+    if (check_op(op_params, dst, src, n) != PPDL_OK) return -1;
+    GemmArgs g;
+    bool im2col;
+    if (!gemm_args_of(op_params, dst, src, &g, &im2col)) return 0;
+    return gemm_ws_bytes_for(g);
+}
 
 extern "C" PPDL_HIP_API int ppdl_hip_supports(const int32_t op_params[16], const ppdl_tview *dst,
                                               const ppdl_tview *src, int nsrc) {
@@ -197,26 +307,14 @@ extern "C" PPDL_HIP_API int ppdl_hip_run(const int32_t op_params[16], const ppdl
     const int32_t *p = op_params;
     hipStream_t s = (hipStream_t)stream;
 
+    GemmArgs g;
+    bool im2col;
+    if (gemm_args_of(p, dst, src, &g, &im2col)) {
+        const GemmWorkspace ws = ws_of(p[13], src, nsrc);
+        return status_of(im2col ? gemm_im2col(g, ws, s) : gemm_dense(g, ws, s));
+    }
+
     switch (p[13]) {
-        case PPDL_OP_CONV:
-        case PPDL_OP_CONV1X1_BA: {
-            const ppdl_tview *x = &src[0], *w = &src[1];
-            const bool fused = p[13] == PPDL_OP_CONV1X1_BA;
-            GemmArgs g{};
-            g.A = (const float *)w->data;
-            g.lda = dst->ne[2];
-            g.B = (const float *)x->data;
-            g.ldb = x->ne[0] * x->ne[1];
-            g.C = (float *)dst->data;
-            g.ldc = dst->ne[0] * dst->ne[1];
-            g.bias = fused ? (const float *)src[2].data : nullptr;
-            g.M = (int)dst->ne[2];
-            g.N = (int)(x->ne[0] * x->ne[1]);
-            g.K = (int)x->ne[2];
-            g.batch = 1;
-            g.act = fused ? p[14] : 0;
-            return status_of(gemm_dense(g, s));
-        }
         case PPDL_OP_BIASACT: {
             const int64_t n = nelem(dst), plane = dst->ne[0] * dst->ne[1];
             return status_of(bias_act((const float *)src[0].data, (const float *)src[1].data,
@@ -230,55 +328,11 @@ extern "C" PPDL_HIP_API int ppdl_hip_run(const int32_t op_params[16], const ppdl
                                        (int)x->ne[1], (int)x->ne[2], TW, TH,
                                        p[13] == PPDL_OP_WG4_INPUT_PAD ? 1 : 0, s));
         }
-        case PPDL_OP_WG4_MADD: {
-            const int64_t T = src[0].ne[0], IC = src[0].ne[1], OC = src[1].ne[0];
-            GemmArgs g{};
-            g.A = (const float *)src[1].data;
-            g.lda = OC;
-            g.sA = IC * OC;
-            g.B = (const float *)src[0].data;
-            g.ldb = T;
-            g.sB = IC * T;
-            g.C = (float *)dst->data;
-            g.ldc = T;
-            g.sC = OC * T;
-            g.bias = nullptr;
-            g.M = (int)OC;
-            g.N = (int)T;
-            g.K = (int)IC;
-            g.batch = 36;
-            g.act = 0;
-            return status_of(gemm_dense(g, s));
-        }
         case PPDL_OP_WG4_OUTPUT: {
             const int OW = (int)dst->ne[0], OH = (int)dst->ne[1], OC = (int)dst->ne[2];
             return status_of(wg4_output((const float *)src[0].data, (const float *)src[1].data,
                                         (float *)dst->data, (OW + 3) / 4, (OH + 3) / 4, OC, OW, OH,
                                         p[14], s));
-        }
-        case PPDL_OP_CONV_IM2COL: {
-            const ppdl_tview *x = &src[0];
-            const int K = p[14] & 0xFF, S = (p[14] >> 8) & 0xFF, P = (p[14] >> 16) & 0xFF;
-            GemmArgs g{};
-            g.A = (const float *)src[1].data;
-            g.lda = dst->ne[2];
-            g.B = (const float *)x->data;
-            g.C = (float *)dst->data;
-            g.ldc = dst->ne[0] * dst->ne[1];
-            g.bias = (const float *)src[2].data;
-            g.M = (int)dst->ne[2];
-            g.N = (int)(dst->ne[0] * dst->ne[1]);
-            g.K = (int)(x->ne[2] * K * K);
-            g.batch = 1;
-            g.act = (p[14] >> 24) & 0xFF;
-            g.IC = (int)x->ne[2];
-            g.IH = (int)x->ne[1];
-            g.IW = (int)x->ne[0];
-            g.OW = (int)dst->ne[0];
-            g.KW = K;
-            g.S = S;
-            g.P = P;
-            return status_of(gemm_im2col(g, s));
         }
         case PPDL_OP_MSDEF:
             return status_of(msdeform((const float *)src[0].data, (const float *)src[1].data,

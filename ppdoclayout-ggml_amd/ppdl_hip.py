@@ -41,6 +41,7 @@ EXPORTS = (
     "ppdl_hip_im2col_f32",
     "ppdl_hip_repack_conv",
     "ppdl_hip_wg4_matrices",
+    "ppdl_hip_workspace_bytes",
 )
 
 
@@ -89,6 +90,8 @@ def lib():
         f64p = ctypes.POINTER(ctypes.c_double)
         L.ppdl_hip_wg4_matrices.argtypes = [f64p, f64p, f64p]
         L.ppdl_hip_wg4_matrices.restype = None
+        L.ppdl_hip_workspace_bytes.argtypes = [i32p, tvp, tvp, ctypes.c_int]
+        L.ppdl_hip_workspace_bytes.restype = ctypes.c_int64
         _lib = L
     return _lib
 
@@ -175,6 +178,19 @@ def supports(op, p14=0, p15=0, dst=None, srcs=()):
         return L.ppdl_hip_supports(params(op, p14, p15), None, None, 0)
     d, arr, n = _views(dst, srcs)
     return L.ppdl_hip_supports(params(op, p14, p15), ctypes.byref(d), arr, n)
+
+
+def workspace_bytes(op, dst, srcs, p14=0, p15=0):
+    """Split-K workspace bytes the node's GEMM plan uses (0: none, -1: invalid node)."""
+    d, arr, n = _views(dst, srcs)
+    return lib().ppdl_hip_workspace_bytes(params(op, p14, p15), ctypes.byref(d), arr, n)
+
+
+def make_workspace(nbytes):
+    """A zero-filled device workspace of at least nbytes (torch int32)."""
+    import torch
+
+    return torch.zeros(max(1, (nbytes + 3) // 4), dtype=torch.int32, device="cuda")
 
 
 def im2col_f32(x, dst, IW, IH, OW, OH, KW, KH, IC, N, ch_stride, img_stride, s0, s1, p0, p1, d0, d1,

@@ -52,6 +52,15 @@ class Node:
         self.name, self.op, self.dst, self.srcs = name, op, dst, srcs
         self.p14, self.p15, self.flops, self.bytes, self.kind = p14, p15, flops, bytes_, kind
 
+    def attach_workspace(self):
+        """Append the split-K workspace this GEMM's plan asks for (zeroed once)."""
+        nb = H.workspace_bytes(self.op, self.dst, self.srcs, self.p14, self.p15)
+        if nb < 0:
+            raise H.PpdlError(f"{self.name}: invalid node")
+        if nb > 0:
+            self.srcs = list(self.srcs) + [H.make_workspace(nb)]
+        return nb
+
     def launch(self, stream):
         rc = H.run(self.op, self.dst, self.srcs, self.p14, self.p15, stream)
         if rc != H.OK:
@@ -122,6 +131,9 @@ class ConvSuite:
                                bytes_=f32 * (13125 * 256 + 300 * (192 + 96 + 4) + 300 * 256)))
         if keep_host:
             self.host["c4"] = (val, off, awr, ref, out)
+        for n in self.nodes:
+            if n.kind == "gemm":
+                n.attach_workspace()
         torch.cuda.synchronize()
 
     def run(self, stream):

@@ -140,3 +140,26 @@ def test_no_cuda_compat_layer(src):
     text = open(src).read()
     for banned in ("__HIP_PLATFORM_NVIDIA__", "cuda_runtime", "#ifdef __CUDACC__", "hipify"):
         assert banned not in text, (src, banned)
+
+
+def test_workspace_query_is_host_only(hip, monkeypatch):
+    v = lambda ne: hip.raw_view(FAKE, ne)  # noqa: E731
+    # a plan pinned to 4 K splits asks for 4 fp32 partial planes
+    monkeypatch.setenv("PPDL_GEMM_TILE", "3,4")
+    big = hip.workspace_bytes(hip.OP_CONV1X1_BA, v([25, 25, 1024]), [v([25, 25, 3328]), v([1024, 3328, 1]), v([1024])], 1)
+    assert big == 4 * 1024 * 625 * 4
+    # a workspace already attached is ignored by the query
+    again = hip.workspace_bytes(hip.OP_CONV1X1_BA, v([25, 25, 1024]),
+                                [v([25, 25, 3328]), v([1024, 3328, 1]), v([1024]), v([big // 4])], 1)
+    assert again == big
+    # tiny GEMM (one k tile): no split even when asked
+    assert hip.workspace_bytes(hip.OP_CONV1X1_BA, v([4, 4, 8]), [v([4, 4, 8]), v([8, 8, 1]), v([8])], 0) == 0
+    # non-GEMM op: none; invalid node: -1
+    assert hip.workspace_bytes(hip.OP_BIASACT, v([4, 4, 8]), [v([4, 4, 8]), v([8])], 0) == 0
+    assert hip.workspace_bytes(hip.OP_CONV1X1_BA, v([4, 4, 9]), [v([4, 4, 8]), v([8, 8, 1]), v([8])], 0) == -1
+
+
+def test_misaligned_workspace_rejected(hip):
+    v = lambda ne, p=FAKE: hip.raw_view(p, ne)  # noqa: E731
+    srcs = [v([25, 25, 64]), v([32, 64, 1]), v([32]), v([1024], FAKE + 4)]
+    assert hip.run(hip.OP_CONV1X1_BA, v([25, 25, 32]), srcs, 0, stream=0) == hip.EINVAL

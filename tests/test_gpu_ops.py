@@ -56,16 +56,26 @@ def conv_inputs(rng, IC, H, W, OC, K):
 
 
 # ---------------------------------------------------------------- HIP paths
-def hip_conv1x1(hip, x, w, b, act):
+def with_ws(hip, op, dst, srcs, p14=0, p15=0, use_ws=True):
+    """srcs plus the split-K workspace the op's plan asks for (if any)."""
+    if not use_ws:
+        return list(srcs)
+    nb = hip.workspace_bytes(op, dst, srcs, p14, p15)
+    assert nb >= 0
+    return list(srcs) + ([hip.make_workspace(nb)] if nb > 0 else [])
+
+
+def hip_conv1x1(hip, x, w, b, act, use_ws=True):
     wr, _ = hip.repack_conv(w)
     OC = w.shape[0]
     xt, wt, bt = dev(x), dev(wr), dev(b)
     out = torch.empty((OC,) + x.shape[1:], device="cuda")
-    hip.run_checked(hip.OP_CONV1X1_BA, out, [xt, wt, bt], act)
+    srcs = with_ws(hip, hip.OP_CONV1X1_BA, out, [xt, wt, bt], act, 0, use_ws)
+    hip.run_checked(hip.OP_CONV1X1_BA, out, srcs, act)
     return out, (xt, wt, bt)
 
 
-def hip_winograd(hip, x, w, b, act, prepadded=False):
+def hip_winograd(hip, x, w, b, act, prepadded=False, use_ws=True):
     IC, H, W = x.shape
     OC = w.shape[0]
     TW, TH = (W + 3) // 4, (H + 3) // 4
@@ -81,18 +91,20 @@ def hip_winograd(hip, x, w, b, act, prepadded=False):
         hip.run_checked(hip.OP_WG4_INPUT, dt, [dev(xp)], T, TH)
     else:
         hip.run_checked(hip.OP_WG4_INPUT_PAD, dt, [dev(x)], T, TH)
-    hip.run_checked(hip.OP_WG4_MADD, yt, [dt, wt])
+    hip.run_checked(hip.OP_WG4_MADD, yt, with_ws(hip, hip.OP_WG4_MADD, yt, [dt, wt], use_ws=use_ws))
     hip.run_checked(hip.OP_WG4_OUTPUT, out, [yt, bt], act, TW)
     return out, dt, yt, wg4
 
 
-def hip_conv_im2col(hip, x, w, b, K, S, P, act):
+def hip_conv_im2col(hip, x, w, b, K, S, P, act, use_ws=True):
     wr, _ = hip.repack_conv(w)
     IC, IH, IW = x.shape
     OC = w.shape[0]
     OH, OW = (IH + 2 * P - K) // S + 1, (IW + 2 * P - K) // S + 1
     out = torch.empty((OC, OH, OW), device="cuda")
-    hip.run_checked(hip.OP_CONV_IM2COL, out, [dev(x), dev(wr), dev(b)], K | (S << 8) | (P << 16) | (act << 24))
+    p14 = K | (S << 8) | (P << 16) | (act << 24)
+    srcs = with_ws(hip, hip.OP_CONV_IM2COL, out, [dev(x), dev(wr), dev(b)], p14, 0, use_ws)
+    hip.run_checked(hip.OP_CONV_IM2COL, out, srcs, p14)
     return out
 
 
@@ -106,9 +118,10 @@ def test_conv1x1_config1(hip, orc):
     ref = orc.conv2d_ref(x, w, b, 1, 0, 1)
     assert normwise(y, ref) < TOL, normwise(y, ref)
     # op 3 (GEMM) then op 5 (bias+act) reproduces the fused op bit for bit
+    # when both run the same GEMM plan (same split-K summation order)
     g = torch.empty_like(out)
     r = torch.empty_like(out)
-    hip.run_checked(hip.OP_CONV, g, [xt, wt, bt], 1)
+    hip.run_checked(hip.OP_CONV, g, with_ws(hip, hip.OP_CONV, g, [xt, wt, bt], 1), 1)
     hip.run_checked(hip.OP_BIASACT, r, [g, bt], 1)
     assert np.array_equal(host(r), y)
     # op 3 alone is the bias-free GEMM
@@ -234,6 +247,68 @@ def test_conv_golden_fixtures_on_gpu(hip, orc):
         else:
             y = host(hip_conv_im2col(hip, x, w, b, K, S, P, act))
         assert normwise(y, f["y"]) < TOL, path
+
+
+# ---------------------------------------------------------------- split-K
+SPLIT_SHAPES = [  # long K, few output tiles: the planner splits K
+    ("conv1x1", (3328, 25, 25, 1024, 1, 1, 0)),
+    ("conv1x1", (1664, 50, 50, 512, 1, 1, 0)),
+    ("im2col", (256, 50, 50, 256, 3, 2, 1)),
+    ("im2col", (64, 13, 11, 40, 3, 2, 1)),
+]
+
+
+@pytest.mark.parametrize("kind,shape", SPLIT_SHAPES)
+@pytest.mark.parametrize("plan", ["3,4", "0,3", "5,2"])
+def test_split_k_matches_unsplit_and_is_deterministic(hip, orc, kind, shape, plan, monkeypatch):
+    """Split-K pinned to several (block shape, splits) plans; one workspace
+    reused for several launches: every launch must write the whole output
+    (NaN-filled before each run), identically each time, and agree with the
+    unsplit GEMM and the oracle."""
+    monkeypatch.setenv("PPDL_GEMM_TILE", plan)
+    IC, H, W, OC, K, S, P = shape
+    say(f"split-K {kind} {IC}->{OC} @{H}x{W}")
+    rng = np.random.default_rng(IC + OC)
+    x, w, b = conv_inputs(rng, IC, H, W, OC, K)
+    wr, _ = hip.repack_conv(w)
+    xt, wt, bt = dev(x), dev(wr), dev(b)
+    OH, OW = (H + 2 * P - K) // S + 1, (W + 2 * P - K) // S + 1
+    out = torch.empty((OC, OH, OW), device="cuda")
+    if kind == "conv1x1":
+        op, p14 = hip.OP_CONV1X1_BA, 2
+    else:
+        op, p14 = hip.OP_CONV_IM2COL, K | (S << 8) | (P << 16) | (2 << 24)
+    nb = hip.workspace_bytes(op, out, [xt, wt, bt], p14)
+    assert nb > 0, "the planner should split this shape"
+    ws = hip.make_workspace(nb)
+    runs = []
+    for _ in range(3):
+        out.fill_(float("nan"))
+        hip.run_checked(op, out, [xt, wt, bt, ws], p14)
+        runs.append(host(out).copy())
+    out.fill_(float("nan"))
+    hip.run_checked(op, out, [xt, wt, bt], p14)  # no workspace: the same block shape unsplit
+    unsplit = host(out)
+    ref = orc.conv2d_ref(x, w, b, S, P, 2)
+    assert not np.isnan(runs[0]).any() and not np.isnan(runs[2]).any()
+    assert np.array_equal(runs[0], runs[1]) and np.array_equal(runs[1], runs[2]), "split-K must be deterministic"
+    assert normwise(runs[0], ref) < TOL
+    assert normwise(unsplit, ref) < TOL
+
+
+def test_workspace_too_small_falls_back(hip, orc, monkeypatch):
+    monkeypatch.setenv("PPDL_GEMM_TILE", "3,8")
+    rng = np.random.default_rng(6)
+    x, w, b = conv_inputs(rng, 1024, 25, 25, 512, 1)
+    wr, _ = hip.repack_conv(w)
+    xt, wt, bt = dev(x), dev(wr), dev(b)
+    out = torch.empty((512, 25, 25), device="cuda")
+    nb = hip.workspace_bytes(hip.OP_CONV1X1_BA, out, [xt, wt, bt], 0)
+    assert nb > 0
+    small = hip.make_workspace(nb // 3)
+    out.fill_(float("nan"))
+    hip.run_checked(hip.OP_CONV1X1_BA, out, [xt, wt, bt, small], 0)
+    assert normwise(host(out), orc.conv2d_ref(x, w, b, 1, 0, 0)) < TOL
 
 
 # ---------------------------------------------------------------- bias + act
