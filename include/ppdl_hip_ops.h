@@ -98,15 +98,20 @@ PPDL_HIP_API int ppdl_hip_supports(const int32_t op_params[16], const ppdl_tview
  *               yt[p][oc][t] = sum_ic dt[p][ic][t] * wg4[p][ic][oc].
  *  1  MASKBOX   src: mask logits ne(40000,NQ); dst ne(4,NQ).
  *  13 TOPK      src: class logits ne(NC,NTOK), NTOK <= 13312; dst I32 ne(NQ).
- *  14 CONV1X1_BA as op 3 plus bias/act: params[14] = act.
+ *  14 CONV1X1_BA as op 3 plus bias/act: params[14] = act; params[15] = add
+ *               mode: 0 none, 1 dst = act(conv + bias + src[3]), 2 dst =
+ *               act(conv + bias) + src[3]; src[3] has dst's shape.
  *  15 WG4_INPUT_PAD as op 10 but src is the unpadded x ne(W,H,IC) and the
  *               conv's zero pad of 1 is applied while reading.
  *  16 CONV_IM2COL src: x ne(IW,IH,IC), wr ne(OC,IC,K*K), bias ne(OC);
- *               params[14] = K | S<<8 | P<<16 | act<<24; dst ne(OW,OH,OC),
- *               OW = (IW+2P-K)/S+1.
+ *               params[14] = K | S<<8 | P<<16 | act<<24; params[15] = PE, an
+ *               extra zero pad after the last column and row (the
+ *               reference's ggml_pad before its k2 convs); dst ne(OW,OH,OC),
+ *               OW = (IW+2P+PE-K)/S+1.
  *
  * Split-K workspace (ops 3, 12, 14, 16): one optional extra src after the
- * op's own (src[3] for 3/14/16, src[2] for 12), a 16-byte aligned contiguous
+ * op's own (src[3] for 3/14/16, src[4] for 14 with an add, src[2] for 12),
+ * a 16-byte aligned contiguous
  * buffer of ppdl_hip_workspace_bytes() bytes; its contents are scratch (no
  * initialisation needed).  Without it, or when it is smaller, the GEMM runs
  * with fewer or no K splits: results differ only by fp32 summation order, and

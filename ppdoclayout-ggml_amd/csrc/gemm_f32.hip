@@ -43,9 +43,13 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 constexpr int kThreads = 256;
 constexpr int kBK = 32;
 
+// 0 none, 1 ReLU, 2 SiLU, 3 GELU (erf form), 4 sigmoid — ggml's relu /
+// silu / gelu_erf / sigmoid
 __device__ __forceinline__ float act_f(float v, int act) {
     if (act == 1) return v > 0.0f ? v : 0.0f;
     if (act == 2) return v / (1.0f + expf(-v));
+    if (act == 3) return 0.5f * v * (1.0f + erff(v * 0.70710678118654752f));
+    if (act == 4) return 1.0f / (1.0f + expf(-v));
     return v;
 }
 
@@ -79,15 +83,17 @@ struct Stage {
     uint32_t ok1;  // im2col: bit e set when element e is inside the image
 };
 
-// BMODE 0: dense B; BMODE 1: implicit im2col B
-template <int BM, int BN, int WGM, int BMODE, bool SPLIT>
+// AMODE 0: A k-major; AMODE 1: A row-major (K % 4 == 0, lda % 4 == 0).
+// BMODE 0: dense B; BMODE 1: implicit im2col B.
+template <int BM, int BN, int WGM, int AMODE, int BMODE, bool SPLIT>
 __global__ __launch_bounds__(kThreads) void k_gemm(GemmArgs g, SplitArgs sp, int tiles_m, int tiles_mn) {
     constexpr int WGN = 4 / WGM;
     constexpr int WM = BM / WGM, WN = BN / WGN;
     constexpr int TM = WM / 32, TN = WN / 32;
     constexpr int PA = BM + 4, PB = BN + 4;
-    // A: float4 along m; threads per k row = BM/4
-    constexpr int TA = BM / 4, RA = kThreads / TA, EA = kBK / RA;
+    // A k-major: float4 along m, BM/4 threads per k row.  A row-major:
+    // float4 along k, kBK/4 threads per m row, 32 rows per pass.
+    constexpr int TA = BM / 4, RA = kThreads / TA, EA = AMODE == 0 ? kBK / RA : BM / (kThreads / (kBK / 4));
     // B dense: float4 along n; B im2col: one column per thread
     constexpr int TB4 = BN / 4, RB4 = kThreads / TB4, EB4 = BMODE == 0 ? kBK / RB4 : 1;
     constexpr int RB1 = kThreads / BN, EB1 = BMODE == 1 ? kBK / RB1 : 1;
@@ -119,8 +125,10 @@ __global__ __launch_bounds__(kThreads) void k_gemm(GemmArgs g, SplitArgs sp, int
     const float *__restrict__ B = g.B + (int64_t)bz * g.sB;
 
     // ---- loader state ----
-    const int am = (tid % TA) * 4, ak = tid / TA;
+    const int am = (tid % TA) * 4, ak = tid / TA;  // A k-major
     const int gm = m0 + am;
+    const int ak4 = (tid % (kBK / 4)) * 4, amr = tid / (kBK / 4);  // A row-major
+    constexpr int RA1 = kThreads / (kBK / 4);
     const int bn4 = (tid % TB4) * 4, bk4 = tid / TB4;  // dense B
     const int gn4 = n0 + bn4;
     const int bn1 = tid % BN, bk1 = tid / BN;  // im2col B
@@ -173,17 +181,28 @@ __global__ __launch_bounds__(kThreads) void k_gemm(GemmArgs g, SplitArgs sp, int
         constexpr bool EDGE = decltype(edge_tag)::value;
         auto load = [&](St &r, int kt) {
             const int k0 = kt * kBK;
+            if (AMODE == 0) {
 #pragma unroll
-            for (int e = 0; e < EA; e++) {
-                const int k = min(k0 + ak + e * RA, K - 1);
-                const float *row = A + (int64_t)k * g.lda;
-                if (!EDGE) {
-                    r.a[e] = ld4(row + gm);
-                } else {
-                    r.a[e].x = row[min(gm + 0, M - 1)];
-                    r.a[e].y = row[min(gm + 1, M - 1)];
-                    r.a[e].z = row[min(gm + 2, M - 1)];
-                    r.a[e].w = row[min(gm + 3, M - 1)];
+                for (int e = 0; e < EA; e++) {
+                    const int k = min(k0 + ak + e * RA, K - 1);
+                    const float *row = A + (int64_t)k * g.lda;
+                    if (!EDGE) {
+                        r.a[e] = ld4(row + gm);
+                    } else {
+                        r.a[e].x = row[min(gm + 0, M - 1)];
+                        r.a[e].y = row[min(gm + 1, M - 1)];
+                        r.a[e].z = row[min(gm + 2, M - 1)];
+                        r.a[e].w = row[min(gm + 3, M - 1)];
+                    }
+                }
+            } else {
+                // rows clamped into [0, M), k chunks into [0, K): K % 4 == 0,
+                // so a chunk is entirely inside or outside
+                const int k = min(k0 + ak4, K - 4);
+#pragma unroll
+                for (int e = 0; e < EA; e++) {
+                    const int m = min(m0 + amr + e * RA1, M - 1);
+                    r.a[e] = ld4(A + (int64_t)m * g.lda + k);
                 }
             }
             if (BMODE == 0) {
@@ -230,15 +249,28 @@ __global__ __launch_bounds__(kThreads) void k_gemm(GemmArgs g, SplitArgs sp, int
         };
         auto store = [&](const St &r, int buf, int kt) {
             const int k0 = kt * kBK;
+            if (AMODE == 0) {
 #pragma unroll
-            for (int e = 0; e < EA; e++) {
-                float4 v = r.a[e];
-                const bool kin = k0 + ak + e * RA < K;
-                v.x = (kin && (!EDGE || gm + 0 < M)) ? v.x : 0.0f;
-                v.y = (kin && (!EDGE || gm + 1 < M)) ? v.y : 0.0f;
-                v.z = (kin && (!EDGE || gm + 2 < M)) ? v.z : 0.0f;
-                v.w = (kin && (!EDGE || gm + 3 < M)) ? v.w : 0.0f;
-                *reinterpret_cast<float4 *>(&As[buf][ak + e * RA][am]) = v;
+                for (int e = 0; e < EA; e++) {
+                    float4 v = r.a[e];
+                    const bool kin = k0 + ak + e * RA < K;
+                    v.x = (kin && (!EDGE || gm + 0 < M)) ? v.x : 0.0f;
+                    v.y = (kin && (!EDGE || gm + 1 < M)) ? v.y : 0.0f;
+                    v.z = (kin && (!EDGE || gm + 2 < M)) ? v.z : 0.0f;
+                    v.w = (kin && (!EDGE || gm + 3 < M)) ? v.w : 0.0f;
+                    *reinterpret_cast<float4 *>(&As[buf][ak + e * RA][am]) = v;
+                }
+            } else {
+                const bool kin = k0 + ak4 < K;
+#pragma unroll
+                for (int e = 0; e < EA; e++) {
+                    const int mr = amr + e * RA1;
+                    const bool ok = kin && m0 + mr < M;
+                    As[buf][ak4 + 0][mr] = ok ? r.a[e].x : 0.0f;
+                    As[buf][ak4 + 1][mr] = ok ? r.a[e].y : 0.0f;
+                    As[buf][ak4 + 2][mr] = ok ? r.a[e].z : 0.0f;
+                    As[buf][ak4 + 3][mr] = ok ? r.a[e].w : 0.0f;
+                }
             }
             if (BMODE == 0) {
 #pragma unroll
@@ -306,21 +338,60 @@ __global__ __launch_bounds__(kThreads) void k_gemm(GemmArgs g, SplitArgs sp, int
     }
 
     const float *__restrict__ bias = g.bias;
-    const int act = g.act;
+    const int act = g.act, add_mode = g.add_mode, bias_n = g.bias_n;
     float *__restrict__ C = g.C + (int64_t)bz * g.sC;
+    const float *__restrict__ Ad = g.add ? g.add + (int64_t)bz * g.sC : nullptr;
+    auto epi = [&](float v, int m, int n, int64_t idx) {
+        if (bias) v += bias[bias_n ? n : m];
+        if (add_mode == 1) v += Ad[idx];
+        v = act_f(v, act);
+        if (add_mode == 2) v += Ad[idx];
+        return v;
+    };
+    if (!g.c_trans) {
 #pragma unroll
-    for (int j = 0; j < TN; j++) {
-        const int n = n0 + wn0 + j * 32 + l32;
-        if (n < N) {
+        for (int j = 0; j < TN; j++) {
+            const int n = n0 + wn0 + j * 32 + l32;
+            if (n < N) {
 #pragma unroll
-            for (int i = 0; i < TM; i++) {
+                for (int i = 0; i < TM; i++) {
 #pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const int m = m0 + wm0 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                    if (m < M) {
-                        float v = acc[i][j][r];
-                        if (bias) v += bias[m];
-                        C[(int64_t)m * g.ldc + n] = act_f(v, act);
+                    for (int r = 0; r < 16; r++) {
+                        const int m = m0 + wm0 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                        if (m < M) {
+                            const int64_t idx = (int64_t)m * g.ldc + n;
+                            C[idx] = epi(acc[i][j][r], m, n, idx);
+                        }
+                    }
+                }
+            }
+        }
+    } else {
+        // C[n][m]: registers 4g..4g+3 hold 4 consecutive m of one n
+        const bool vec_ok = (g.ldc % 4 == 0) && ((((uintptr_t)C) & 15) == 0) &&
+                            (!Ad || ((((uintptr_t)Ad) & 15) == 0));
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+            const int n = n0 + wn0 + j * 32 + l32;
+            if (n < N) {
+#pragma unroll
+                for (int i = 0; i < TM; i++) {
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        const int mb = m0 + wm0 + i * 32 + 8 * q + 4 * (lane >> 5);
+                        const int64_t idx = (int64_t)n * g.ldc + mb;
+                        if (vec_ok && mb + 3 < M) {
+                            float4 v;
+                            v.x = epi(acc[i][j][4 * q + 0], mb + 0, n, idx + 0);
+                            v.y = epi(acc[i][j][4 * q + 1], mb + 1, n, idx + 1);
+                            v.z = epi(acc[i][j][4 * q + 2], mb + 2, n, idx + 2);
+                            v.w = epi(acc[i][j][4 * q + 3], mb + 3, n, idx + 3);
+                            *reinterpret_cast<float4 *>(C + idx) = v;
+                        } else {
+#pragma unroll
+                            for (int u = 0; u < 4; u++)
+                                if (mb + u < M) C[idx + u] = epi(acc[i][j][4 * q + u], mb + u, n, idx + u);
+                        }
                     }
                 }
             }
@@ -328,34 +399,36 @@ __global__ __launch_bounds__(kThreads) void k_gemm(GemmArgs g, SplitArgs sp, int
     }
 }
 
-// Split-K fix-up: C = act(sum_{s=0..S-1} P[s] + bias), s ascending.  C is
-// contiguous per batch plane (ldc == N, sC == M*N) for every op that splits.
+// Split-K fix-up: the GEMM epilogue applied to sum_{s=0..S-1} P[s], s
+// ascending.  Partials are [s][batch][M][N]; VEC = 4 needs a plain C with
+// ldc == N (four consecutive n share m).
 template <int VEC>
 __global__ __launch_bounds__(256) void k_splitk_reduce(const float *__restrict__ P, int S, int64_t total,
-                                                       int64_t MN, int N, int M, const float *__restrict__ bias,
-                                                       int act, float *__restrict__ C) {
+                                                       GemmArgs g) {
     const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * VEC;
     if (i >= total) return;
-    const int m = (int)((i % MN) / N);
-    const float b = bias ? bias[m] : 0.0f;
-    if (VEC == 4) {
-        float4 v = *reinterpret_cast<const float4 *>(P + i);
-        for (int s = 1; s < S; s++) {
-            const float4 u = *reinterpret_cast<const float4 *>(P + s * total + i);
-            v.x += u.x;
-            v.y += u.y;
-            v.z += u.z;
-            v.w += u.w;
-        }
-        v.x = act_f(v.x + b, act);
-        v.y = act_f(v.y + b, act);
-        v.z = act_f(v.z + b, act);
-        v.w = act_f(v.w + b, act);
-        *reinterpret_cast<float4 *>(C + i) = v;
-    } else {
-        float v = P[i];
-        for (int s = 1; s < S; s++) v += P[s * total + i];
-        C[i] = act_f(v + b, act);
+    const int64_t MN = (int64_t)g.M * g.N;
+    const int bz = (int)(i / MN);
+    const int64_t rem = i - (int64_t)bz * MN;
+    const int m = (int)(rem / g.N), n = (int)(rem - (int64_t)m * g.N);
+    float v[VEC];
+#pragma unroll
+    for (int u = 0; u < VEC; u++) v[u] = P[i + u];
+    for (int s = 1; s < S; s++)
+#pragma unroll
+        for (int u = 0; u < VEC; u++) v[u] += P[s * total + i + u];
+    float *C = g.C + (int64_t)bz * g.sC;
+    const float *Ad = g.add ? g.add + (int64_t)bz * g.sC : nullptr;
+#pragma unroll
+    for (int u = 0; u < VEC; u++) {
+        const int nn = n + u;
+        const int64_t idx = g.c_trans ? (int64_t)nn * g.ldc + m : (int64_t)m * g.ldc + nn;
+        float x = v[u];
+        if (g.bias) x += g.bias[g.bias_n ? nn : m];
+        if (g.add_mode == 1) x += Ad[idx];
+        x = act_f(x, g.act);
+        if (g.add_mode == 2) x += Ad[idx];
+        C[idx] = x;
     }
 }
 
@@ -409,7 +482,7 @@ int env_override(int *cfg, int *splits) {
     return 1;
 }
 
-template <int BM, int BN, int WGM, int BMODE>
+template <int BM, int BN, int WGM, int AMODE, int BMODE>
 hipError_t launch(const GemmArgs &g, int S, const GemmWorkspace &ws, hipStream_t s) {
     const int tiles_m = (g.M + BM - 1) / BM, tiles_n = (g.N + BN - 1) / BN;
     const int64_t tiles = (int64_t)tiles_m * tiles_n * g.batch;
@@ -421,21 +494,21 @@ hipError_t launch(const GemmArgs &g, int S, const GemmWorkspace &ws, hipStream_t
         sp.splits = S;
         sp.ktiles_per_split = (nk + S - 1) / S;
         sp.partials = (float *)ws.base;
-        hipLaunchKernelGGL((k_gemm<BM, BN, WGM, BMODE, true>), dim3((unsigned)total), dim3(kThreads), 0, s, g,
-                           sp, tiles_m, tiles_m * tiles_n);
+        hipLaunchKernelGGL((k_gemm<BM, BN, WGM, AMODE, BMODE, true>), dim3((unsigned)total), dim3(kThreads), 0,
+                           s, g, sp, tiles_m, tiles_m * tiles_n);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
-        const int64_t MN = (int64_t)g.M * g.N, n = MN * g.batch;
-        const bool vec = (g.N % 4 == 0) && ((((uintptr_t)g.C) & 15) == 0);
+        const int64_t n = (int64_t)g.M * g.N * g.batch;
+        const bool vec = !g.c_trans && g.ldc == g.N && (g.N % 4 == 0) && ((((uintptr_t)g.C) & 15) == 0);
         if (vec)
             hipLaunchKernelGGL(k_splitk_reduce<4>, dim3((unsigned)((n / 4 + 255) / 256)), dim3(256), 0, s,
-                               sp.partials, S, n, MN, g.N, g.M, g.bias, g.act, g.C);
+                               sp.partials, S, n, g);
         else
             hipLaunchKernelGGL(k_splitk_reduce<1>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
-                               sp.partials, S, n, MN, g.N, g.M, g.bias, g.act, g.C);
+                               sp.partials, S, n, g);
     } else {
-        hipLaunchKernelGGL((k_gemm<BM, BN, WGM, BMODE, false>), dim3((unsigned)total), dim3(kThreads), 0, s,
-                           g, sp, tiles_m, tiles_m * tiles_n);
+        hipLaunchKernelGGL((k_gemm<BM, BN, WGM, AMODE, BMODE, false>), dim3((unsigned)total), dim3(kThreads), 0,
+                           s, g, sp, tiles_m, tiles_m * tiles_n);
     }
     return hipGetLastError();
 }
@@ -443,13 +516,21 @@ hipError_t launch(const GemmArgs &g, int S, const GemmWorkspace &ws, hipStream_t
 template <int BMODE>
 hipError_t dispatch(const GemmArgs &g, const GemmWorkspace &ws, hipStream_t s) {
     const GemmPlan p = gemm_plan(g, ws.bytes);
+    if (g.a_rowmajor) {
+        // row-major A (token-major activations) is built for the two block
+        // shapes the planner uses
+        if (BMODE != 0 || g.K % 4 != 0 || g.lda % 4 != 0 || (((uintptr_t)g.A) & 15) != 0)
+            return hipErrorInvalidValue;
+        if (p.cfg == 5) return launch<32, 128, 1, 1, 0>(g, p.splits, ws, s);
+        return launch<64, 64, 2, 1, 0>(g, p.splits, ws, s);
+    }
     switch (p.cfg) {
-        case 0: return launch<128, 128, 2, BMODE>(g, p.splits, ws, s);
-        case 1: return launch<64, 128, 2, BMODE>(g, p.splits, ws, s);
-        case 2: return launch<128, 64, 2, BMODE>(g, p.splits, ws, s);
-        case 3: return launch<64, 64, 2, BMODE>(g, p.splits, ws, s);
-        case 4: return launch<32, 256, 1, BMODE>(g, p.splits, ws, s);
-        default: return launch<32, 128, 1, BMODE>(g, p.splits, ws, s);
+        case 0: return launch<128, 128, 2, 0, BMODE>(g, p.splits, ws, s);
+        case 1: return launch<64, 128, 2, 0, BMODE>(g, p.splits, ws, s);
+        case 2: return launch<128, 64, 2, 0, BMODE>(g, p.splits, ws, s);
+        case 3: return launch<64, 64, 2, 0, BMODE>(g, p.splits, ws, s);
+        case 4: return launch<32, 256, 1, 0, BMODE>(g, p.splits, ws, s);
+        default: return launch<32, 128, 1, 0, BMODE>(g, p.splits, ws, s);
     }
 }
 

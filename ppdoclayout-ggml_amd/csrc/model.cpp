@@ -1,0 +1,1000 @@
+// PP-DocLayoutV3 on MI355X: the reference's graph (src/ppdoclayout.cpp:363-883)
+// rebuilt as a list of kernel launches over device buffers, captured once
+// into a hipGraph and replayed per image.
+//
+//  * Weights come from the reference's GGUF (F32, BN folded) and are repacked
+//    at load (src/ppdoclayout.cpp:251-346) through ppdl_hip_repack_conv.
+//  * Every conv goes through the tagged-op C-ABI (ppdl_hip_run), chosen by
+//    the same router as builder::conv (src/ppdoclayout.cpp:388-543): 1x1 ->
+//    op 14, k3 s1 p1 -> ops 15/12/11 (F(4,3)), k2 / k3 s2 -> op 16,
+//    depthwise -> the stock depthwise kernel.  MSDeformAttn, mask->box and
+//    top-300 are ops 2, 1 and 13.
+//  * Stock ops (linears, layer norm, attention, interpolation, ...) use this
+//    library's own kernels; concats cost nothing: producers write straight
+//    into their channel slice of the concatenated buffer.
+#include <hip/hip_runtime.h>
+#include <sys/stat.h>
+
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <functional>
+#include <map>
+#include <memory>
+#include <numeric>
+#include <string>
+#include <vector>
+
+#include "../../include/ppdl_hip_ops.h"
+#include "../../include/ppdoclayout.h"
+#include "gguf.h"
+#include "net_internal.h"
+
+namespace ppdl {
+namespace {
+
+constexpr int IMG = 800, NQ = 300, NC = 25, NTOK = kNTOK, NPIX = kMaskPix;
+
+struct Img {
+    float *d = nullptr;
+    int C = 0, H = 0, W = 0;
+};
+struct Seq {
+    float *d = nullptr;
+    int T = 0, D = 0, ld = 0;  // token-major rows of D features, row stride ld
+};
+
+struct Node {
+    std::string name;
+    int kernels;  // device kernels this node launches
+    std::function<int(hipStream_t)> run;
+};
+
+struct DumpRec {
+    std::string name;
+    const void *d;
+    std::vector<int64_t> ne;
+    bool i32;
+};
+
+bool ends_with(const std::string &s, const char *suf) {
+    const size_t n = strlen(suf);
+    return s.size() >= n && s.compare(s.size() - n, n, suf) == 0;
+}
+
+ppdl_tview view(const void *d, std::vector<int64_t> ne, int32_t type = PPDL_TYPE_F32) {
+    ppdl_tview v;
+    v.data = const_cast<void *>(d);
+    while (ne.size() < 4) ne.push_back(1);
+    int64_t nb = 4;
+    for (int i = 0; i < 4; i++) {
+        v.ne[i] = ne[i];
+        v.nb[i] = nb;
+        nb *= ne[i];
+    }
+    v.type = type;
+    return v;
+}
+ppdl_tview view(const Img &x) { return view(x.d, {x.W, x.H, x.C}); }
+
+std::vector<int32_t> op_params(int op, int p14, int p15) {
+    std::vector<int32_t> v(16, 0);
+    v[12] = (int32_t)PPDL_MAGIC;
+    v[13] = op;
+    v[14] = p14;
+    v[15] = p15;
+    return v;
+}
+
+alignas(16) const float kShapeOnly[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+
+class Net {
+   public:
+    ~Net() {
+        if (exec_) (void)hipGraphExecDestroy(exec_);
+        if (graph_) (void)hipGraphDestroy(graph_);
+        if (stream_) (void)hipStreamDestroy(stream_);
+        for (void *p : allocs_) (void)hipFree(p);
+    }
+
+    bool load(const std::string &path, std::string *err);
+    bool build(bool dumps, std::string *err);
+    bool capture(std::string *err);
+    int replay();  // one graph launch + sync
+    double time_graph(int iters);
+    bool upload_image(const float *host);
+
+    int nodes() const {
+        int k = 0;
+        for (const auto &n : nodes_) k += n.kernels;
+        return k;
+    }
+
+    // outputs
+    float *logits_ = nullptr, *boxes_ = nullptr, *order_ = nullptr, *masks_ = nullptr, *refu_ = nullptr;
+    int32_t *topk_ = nullptr;
+    std::vector<DumpRec> dumps_;
+
+   private:
+    // ---- memory ----
+    float *alloc(int64_t nfloat) {
+        void *p = nullptr;
+        if (hipMalloc(&p, (size_t)std::max<int64_t>(nfloat, 1) * 4) != hipSuccess) {
+            oom_ = true;
+            return nullptr;
+        }
+        allocs_.push_back(p);
+        return (float *)p;
+    }
+    float *upload(const std::vector<float> &h) {
+        float *d = alloc((int64_t)h.size());
+        if (d && hipMemcpy(d, h.data(), h.size() * 4, hipMemcpyHostToDevice) != hipSuccess) oom_ = true;
+        return d;
+    }
+    const float *W(const std::string &name) {
+        auto it = w_.find(name);
+        if (it == w_.end()) {
+            if (missing_.empty()) missing_ = name;
+            return nullptr;
+        }
+        return it->second;
+    }
+    const std::vector<int64_t> &shape(const std::string &name) {
+        static const std::vector<int64_t> none = {1, 1, 1, 1};
+        auto it = ne_.find(name);
+        if (it == ne_.end()) {
+            if (missing_.empty()) missing_ = name;
+            return none;
+        }
+        return it->second;
+    }
+    void dump(const char *name, const void *d, std::vector<int64_t> ne, bool i32 = false) {
+        if (want_dumps_) dumps_.push_back({name, d, ne, i32});
+    }
+    void dump(const char *name, const Img &x) { dump(name, x.d, {x.W, x.H, x.C}); }
+
+    // ---- node emission ----
+    void node(const std::string &name, int kernels, std::function<int(hipStream_t)> fn) {
+        nodes_.push_back({name, kernels, std::move(fn)});
+    }
+    // one tagged op through the C-ABI; a GEMM op gets the shared split-K
+    // workspace appended when its plan asks for one
+    void tagged(const std::string &name, int op, int p14, int p15, ppdl_tview dst, std::vector<ppdl_tview> src) {
+        const std::vector<int32_t> pv = op_params(op, p14, p15);
+        const int64_t wsb = ppdl_hip_workspace_bytes(pv.data(), &dst, src.data(), (int)src.size());
+        if (wsb < 0) {
+            if (bad_node_.empty()) bad_node_ = name;
+            return;
+        }
+        ws_need_ = std::max(ws_need_, wsb);
+        const int kernels = (op == PPDL_OP_WG4_INPUT_PAD || op == PPDL_OP_WG4_OUTPUT) ? 1 : (wsb > 0 ? 2 : 1);
+        node(name, kernels, [this, pv, dst, src, wsb](hipStream_t s) {
+            std::vector<ppdl_tview> sv = src;
+            if (wsb > 0) sv.push_back(view(ws_, {(ws_bytes_ + 3) / 4}));
+            return ppdl_hip_run(pv.data(), &dst, sv.data(), (int)sv.size(), s);
+        });
+    }
+    void gemm(const std::string &name, GemmArgs g) {
+        const int64_t wsb = gemm_ws_bytes_for(g);
+        ws_need_ = std::max(ws_need_, wsb);
+        node(name, wsb > 0 ? 2 : 1, [this, g, wsb](hipStream_t s) {
+            GemmWorkspace ws{wsb > 0 ? ws_ : nullptr, wsb > 0 ? ws_bytes_ : 0};
+            return gemm_dense(g, ws, s) == hipSuccess ? 0 : 3;
+        });
+    }
+    static int ok(hipError_t e) { return e == hipSuccess ? 0 : 3; }
+
+    // ---- layers ----
+    Img conv(const Img &x, const std::string &name, int s, int p, int act, float *out = nullptr, int pad_end = 0,
+             const float *add = nullptr, int add_mode = 0);
+    Seq lin(const Seq &x, const std::string &name, int act, float *out = nullptr, const float *add = nullptr,
+            int add_mode = 0);
+    Seq ln(const Seq &a, const float *b, const std::string &name, float *out = nullptr, int out_chw = 0);
+    Seq mlp3(const Seq &x, const std::string &pfx);
+    Seq mha(const Seq &qk_in, const Seq &v_in, const std::string &pfx, float *out, const float *resid);
+    void hg_block(const Img &cat, int cin, const std::string &pfx, bool light, int mid, Img *y, float *out,
+                  const float *resid);
+    Img csp(const Img &x, const std::string &pfx, float *out);
+
+    std::vector<void *> allocs_;
+    std::map<std::string, float *> w_;
+    std::map<std::string, std::vector<int64_t>> ne_;
+    std::vector<Node> nodes_;
+    std::string missing_, bad_node_;
+    bool oom_ = false, want_dumps_ = false;
+    int64_t ws_need_ = 0, ws_bytes_ = 0;
+    void *ws_ = nullptr;
+    float *wg_dt_ = nullptr, *wg_yt_ = nullptr;  // shared F(4,3) intermediates
+    int64_t wg_need_ = 0;
+    hipStream_t stream_ = nullptr;
+    hipGraph_t graph_ = nullptr;
+    hipGraphExec_t exec_ = nullptr;
+    float *image_ = nullptr, *pos_ = nullptr, *valid_ = nullptr;
+};
+
+// ---------------------------------------------------------------------------
+// Loading: read every tensor, repack conv weights (.wr [tap][ic][oc] and, for
+// 3x3, the 36-plane .wg4), store linear weights transposed (.wt [in][out])
+// for the row-major-activation GEMM, keep biases / norms / depthwise weights
+// as they are.  The self-attention q and k projections share their input, so
+// they are also stored side by side (".qk").
+bool Net::load(const std::string &path, std::string *err) {
+    GgufFile g;
+    if (!gguf_open(path, &g, err)) return false;
+    std::vector<float> h;
+    for (const auto &t : g.tensors) {
+        h.resize((size_t)t.nelem());
+        if (!gguf_read_f32(g, t, h.data(), err)) return false;
+        ne_[t.name] = t.ne;
+        const std::string base = ends_with(t.name, ".weight") ? t.name.substr(0, t.name.size() - 7) : "";
+        if (!base.empty() && t.ne.size() == 4 && t.ne[3] > 1 && t.ne[2] > 1 && t.ne[0] == t.ne[1] &&
+            t.ne[0] <= 3) {
+            const int64_t K = t.ne[0], IC = t.ne[2], OC = t.ne[3];
+            std::vector<float> wr((size_t)(K * K * IC * OC)), wg4(K == 3 ? (size_t)(36 * IC * OC) : 0);
+            if (ppdl_hip_repack_conv(h.data(), OC, IC, K, wr.data(), K == 3 ? wg4.data() : nullptr) != PPDL_OK) {
+                *err = "repack failed: " + t.name;
+                return false;
+            }
+            w_[base + ".wr"] = upload(wr);
+            if (K == 3) w_[base + ".wg4"] = upload(wg4);
+        } else if (!base.empty() && t.ne.size() == 2) {
+            const int64_t in = t.ne[0], out = t.ne[1];
+            std::vector<float> wt((size_t)(in * out));
+            for (int64_t o = 0; o < out; o++)
+                for (int64_t i = 0; i < in; i++) wt[(size_t)(i * out + o)] = h[(size_t)(o * in + i)];
+            w_[base + ".wt"] = upload(wt);
+        } else {
+            w_[t.name] = upload(h);
+        }
+        if (oom_) {
+            *err = "device allocation failed while loading " + t.name;
+            return false;
+        }
+    }
+    // fused q|k projections
+    std::vector<std::string> att = {"aifi"};
+    for (int i = 0; i < 6; i++) att.push_back("dec" + std::to_string(i) + ".sa");
+    for (const auto &a : att) {
+        if (!g.index.count(a + ".q.weight") || !g.index.count(a + ".k.weight")) continue;
+        const auto &tq = g.tensors[g.index[a + ".q.weight"]];
+        const int64_t in = tq.ne[0], out = tq.ne[1];
+        std::vector<float> q((size_t)(in * out)), k(q.size()), qb((size_t)out), kb((size_t)out);
+        if (!gguf_read_f32(g, tq, q.data(), err) ||
+            !gguf_read_f32(g, g.tensors[g.index[a + ".k.weight"]], k.data(), err) ||
+            !gguf_read_f32(g, g.tensors[g.index[a + ".q.bias"]], qb.data(), err) ||
+            !gguf_read_f32(g, g.tensors[g.index[a + ".k.bias"]], kb.data(), err))
+            return false;
+        std::vector<float> wt((size_t)(in * 2 * out)), b((size_t)(2 * out));
+        for (int64_t o = 0; o < out; o++) {
+            for (int64_t i = 0; i < in; i++) {
+                wt[(size_t)(i * 2 * out + o)] = q[(size_t)(o * in + i)];
+                wt[(size_t)(i * 2 * out + out + o)] = k[(size_t)(o * in + i)];
+            }
+            b[(size_t)o] = qb[(size_t)o];
+            b[(size_t)(out + o)] = kb[(size_t)o];
+        }
+        w_[a + ".qk.wt"] = upload(wt);
+        w_[a + ".qk.bias"] = upload(b);
+        ne_[a + ".qk.weight"] = {in, 2 * out};
+    }
+    if (oom_) {
+        *err = "device allocation failed";
+        return false;
+    }
+    return true;
+}
+
+// ---------------------------------------------------------------------------
+// builder::conv (src/ppdoclayout.cpp:388-543): route by shape.
+Img Net::conv(const Img &x, const std::string &name, int s, int p, int act, float *out, int pad_end,
+              const float *add, int add_mode) {
+    const auto &ne = shape(name + ".weight");  // (K, K, IC, OC)
+    const int K = (int)ne[0], ICw = (int)ne[2], OC = (int)ne[3];
+    const float *b = W(name + ".bias");
+    const int OH = (x.H + 2 * p + pad_end - K) / s + 1, OW = (x.W + 2 * p + pad_end - K) / s + 1;
+    Img y{out ? out : alloc((int64_t)OC * OH * OW), OC, OH, OW};
+    if (ICw == 1 && x.C != 1) {
+        // depthwise: ggml_conv_2d_dw_direct + bias + act (:400-404)
+        const float *w = W(name + ".weight");
+        const Img xi = x;
+        node(name, 1, [=](hipStream_t st) { return ok(dwconv(xi.d, w, b, y.d, xi.C, xi.H, xi.W, K, s, p, act, st)); });
+        return y;
+    }
+    if (ICw != x.C && bad_node_.empty()) bad_node_ = name + " (channel mismatch)";
+    const ppdl_tview vb = view(b, {OC});
+    if (K == 1 && s == 1 && p == 0 && pad_end == 0) {
+        // op 3 + op 5 fused: one GEMM writing CHW with bias/act (:408-423)
+        std::vector<ppdl_tview> src = {view(x), view(W(name + ".wr"), {OC, x.C, 1}), vb};
+        if (add_mode) src.push_back(view(add, {OW, OH, OC}));
+        tagged(name, PPDL_OP_CONV1X1_BA, act, add_mode, view(y), src);
+    } else if (K == 3 && s == 1 && p == 1 && pad_end == 0 && add_mode == 0) {
+        // Winograd F(4,3): pad fused into op 15, madd (op 12), output + bias + act (op 11) (:425-463)
+        const int TW = (OW + 3) / 4, TH = (OH + 3) / 4, T = TW * TH;
+        wg_need_ = std::max(wg_need_, (int64_t)36 * std::max(x.C, OC) * T);
+        // The 36-plane intermediates dt / yt are shared by every Winograd
+        // conv and allocated once the largest is known, so the launches
+        // read their address at run time.  The workspace query only reads
+        // shapes: a host sentinel stands in for their address there.
+        const Img xi = x;
+        const float *wg4 = W(name + ".wg4");
+        const auto p_in = op_params(PPDL_OP_WG4_INPUT_PAD, T, TH), p_md = op_params(PPDL_OP_WG4_MADD, 0, 0),
+                   p_out = op_params(PPDL_OP_WG4_OUTPUT, act, TW);
+        const ppdl_tview qd = view(kShapeOnly, {T, OC, 36});
+        const ppdl_tview qs[2] = {view(kShapeOnly, {T, x.C, 36}), view(wg4, {OC, x.C, 36})};
+        const int64_t wsb = ppdl_hip_workspace_bytes(p_md.data(), &qd, qs, 2);
+        if (wsb < 0 && bad_node_.empty()) bad_node_ = name;
+        ws_need_ = std::max(ws_need_, wsb);
+        node(name + ".wg_in", 1, [=](hipStream_t st) {
+            ppdl_tview d = view(wg_dt_, {T, xi.C, 36}), sx = view(xi);
+            return ppdl_hip_run(p_in.data(), &d, &sx, 1, st);
+        });
+        node(name + ".wg_madd", wsb > 0 ? 2 : 1, [=](hipStream_t st) {
+            ppdl_tview d = view(wg_yt_, {T, OC, 36});
+            std::vector<ppdl_tview> sv = {view(wg_dt_, {T, xi.C, 36}), view(wg4, {OC, xi.C, 36})};
+            if (wsb > 0) sv.push_back(view(ws_, {(ws_bytes_ + 3) / 4}));
+            return ppdl_hip_run(p_md.data(), &d, sv.data(), (int)sv.size(), st);
+        });
+        node(name + ".wg_out", 1, [=](hipStream_t st) {
+            ppdl_tview d = view(y);
+            ppdl_tview sv[2] = {view(wg_yt_, {T, OC, 36}), view(b, {OC})};
+            return ppdl_hip_run(p_out.data(), &d, sv, 2, st);
+        });
+    } else {
+        // k2, k3 s2: implicit-im2col GEMM + bias + act (op 16), replacing
+        // im2col + mul_mat + permute/cont + add + act (:535-542)
+        tagged(name, PPDL_OP_CONV_IM2COL, K | (s << 8) | (p << 16) | (act << 24), pad_end, view(y),
+               {view(x), view(W(name + ".wr"), {OC, x.C, K * K}), vb});
+    }
+    return y;
+}
+
+// lin (:545-548): y = x W^T + b as a row-major-activation GEMM; optional act
+// and fused add (residual) in the epilogue.
+Seq Net::lin(const Seq &x, const std::string &name, int act, float *out, const float *add, int add_mode) {
+    const auto &ne = shape(name + ".weight");  // (in, out)
+    const int in = (int)ne[0], nout = (int)ne[1];
+    if (in != x.D && bad_node_.empty()) bad_node_ = name + " (feature mismatch)";
+    Seq y{out ? out : alloc((int64_t)x.T * nout), x.T, nout, nout};
+    GemmArgs g{};
+    g.A = x.d;
+    g.lda = x.ld;
+    g.a_rowmajor = 1;
+    g.B = W(name + ".wt");
+    g.ldb = nout;
+    g.C = y.d;
+    g.ldc = nout;
+    g.bias = W(name + ".bias");
+    g.bias_n = 1;
+    g.M = x.T;
+    g.N = nout;
+    g.K = in;
+    g.batch = 1;
+    g.act = act;
+    g.add = add;
+    g.add_mode = add_mode;
+    gemm(name, g);
+    return y;
+}
+
+// ln (:550-554): LN(a + b) * w + bias
+Seq Net::ln(const Seq &a, const float *b, const std::string &name, float *out, int out_chw) {
+    Seq y{out ? out : alloc((int64_t)a.T * kDM), a.T, kDM, kDM};
+    const float *gm = W(name + ".weight"), *bt = W(name + ".bias");
+    const Seq ai = a;
+    node(name, 1, [=](hipStream_t st) { return ok(layernorm(ai.d, b, gm, bt, y.d, ai.T, out_chw, st)); });
+    return y;
+}
+
+Seq Net::mlp3(const Seq &x, const std::string &pfx) {
+    Seq h = lin(x, pfx + ".0", kActRelu);
+    h = lin(h, pfx + ".1", kActRelu);
+    return lin(h, pfx + ".2", kActNone);
+}
+
+// mha (:572-587) + output projection; out = x_resid + o(attn) when resid given
+Seq Net::mha(const Seq &qk_in, const Seq &v_in, const std::string &pfx, float *out, const float *resid) {
+    const int T = qk_in.T;
+    Seq qk = lin(qk_in, pfx + ".qk", kActNone);  // [T][512]: q | k
+    Seq v = lin(v_in, pfx + ".v", kActNone);
+    Seq att{alloc((int64_t)T * kDM), T, kDM, kDM};
+    node(pfx + ".attn", 1, [=](hipStream_t st) {
+        return ok(attention(qk.d, 2 * kDM, qk.d + kDM, 2 * kDM, v.d, kDM, att.d, kDM, T, st));
+    });
+    return lin(att, pfx + ".o", kActNone, out, resid, resid ? 2 : 0);
+}
+
+// hg_block (:598-614).  `cat` already holds the block input in its first
+// `cin` channels; each layer writes its output into the next slice.
+void Net::hg_block(const Img &cat, int cin, const std::string &pfx, bool light, int mid, Img *y, float *out,
+                   const float *resid) {
+    Img cur{cat.d, cin, cat.H, cat.W};
+    const int64_t plane = (int64_t)cat.H * cat.W;
+    for (int l = 0; l < 6; l++) {
+        const std::string lp = pfx + ".l" + std::to_string(l);
+        float *slot = cat.d + (cin + (int64_t)l * mid) * plane;
+        if (light) {
+            Img t = conv(cur, lp + ".c1", 1, 0, kActNone);
+            cur = conv(t, lp + ".c2", 1, 2, kActRelu, slot);  // depthwise k5 p2
+        } else {
+            cur = conv(cur, lp, 1, 1, kActRelu, slot);  // k3 p1
+        }
+    }
+    Img full{cat.d, cin + 6 * mid, cat.H, cat.W};
+    Img a = conv(full, pfx + ".agg0", 1, 0, kActRelu);
+    *y = conv(a, pfx + ".agg1", 1, 0, kActRelu, out, 0, resid, resid ? 2 : 0);
+}
+
+// csp (:662-668): a = c1(x); 3x repvgg; b = c2(x); a + b.  repvgg (:656-660)
+// = silu(c1_3x3(a) + c2_1x1(a)); the sums ride in the 1x1 convs' epilogues.
+Img Net::csp(const Img &x, const std::string &pfx, float *out) {
+    Img a = conv(x, pfx + ".c1", 1, 0, kActSilu);
+    for (int i = 0; i < 3; i++) {
+        const std::string bp = pfx + ".bn" + std::to_string(i);
+        Img t = conv(a, bp + ".c1", 1, 1, kActNone);
+        a = conv(a, bp + ".c2", 1, 0, kActSilu, nullptr, 0, t.d, 1);
+    }
+    return conv(x, pfx + ".c2", 1, 0, kActSilu, out, 0, a.d, 2);
+}
+
+// ---------------------------------------------------------------------------
+// The full graph (builder::build, src/ppdoclayout.cpp:733-882).
+bool Net::build(bool dumps, std::string *err) {
+    want_dumps_ = dumps;
+    if (hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking) != hipSuccess) {
+        *err = "hipStreamCreate failed";
+        return false;
+    }
+    image_ = alloc(3LL * IMG * IMG);
+    pos_ = alloc(625LL * kDM);
+    valid_ = alloc(NTOK);
+
+    // ---- backbone (:616-652)
+    Img img{image_, 3, IMG, IMG};
+    Img x = conv(img, "stem1", 2, 1, kActRelu);  // 400, 32
+    dump("stem1", x);
+    Img cat0{alloc(64LL * 400 * 400), 64, 400, 400};  // [maxpool(xp) | stem2b]
+    {
+        const Img xi = x;
+        node("stem.pool", 1, [=](hipStream_t st) { return ok(maxpool2_padend(xi.d, cat0.d, 32, 400, 400, st)); });
+    }
+    Img a = conv(x, "stem2a", 1, 0, kActRelu, nullptr, 1);        // pad(1,1) then k2 -> 400, 16
+    conv(a, "stem2b", 1, 0, kActRelu, cat0.d + 32LL * 400 * 400, 1);  // -> 400, 32
+    x = conv(cat0, "stem3", 2, 1, kActRelu);                        // 200, 32
+    Img cat_s0{alloc((48 + 6 * 48LL) * 200 * 200), 48 + 6 * 48, 200, 200};
+    x = conv(x, "stem4", 1, 0, kActRelu, cat_s0.d);  // 200, 48
+    dump("stem", x);
+
+    Img s0, s1, s2, s3;
+    hg_block(cat_s0, 48, "st0.b0", false, 48, &s0, nullptr, nullptr);  // 200, 128
+    dump("st0", s0);
+    Img cat_s1{alloc((128 + 6 * 96LL) * 100 * 100), 128 + 6 * 96, 100, 100};
+    conv(s0, "st1.ds", 2, 1, kActNone, cat_s1.d);  // dw -> 100, 128
+    hg_block(cat_s1, 128, "st1.b0", false, 96, &s1, nullptr, nullptr);  // 100, 512
+    dump("st1", s1);
+    const int64_t p50 = 50 * 50;
+    Img cat_b0{alloc((512 + 6 * 192LL) * p50), 512 + 6 * 192, 50, 50};
+    Img cat_b1{alloc((1024 + 6 * 192LL) * p50), 1024 + 6 * 192, 50, 50};
+    Img cat_b2{alloc((1024 + 6 * 192LL) * p50), 1024 + 6 * 192, 50, 50};
+    conv(s1, "st2.ds", 2, 1, kActNone, cat_b0.d);  // dw -> 50, 512
+    Img t;
+    hg_block(cat_b0, 512, "st2.b0", true, 192, &t, cat_b1.d, nullptr);         // -> b1 input
+    hg_block(cat_b1, 1024, "st2.b1", true, 192, &t, cat_b2.d, cat_b1.d);       // + residual
+    hg_block(cat_b2, 1024, "st2.b2", true, 192, &s2, nullptr, cat_b2.d);       // + residual
+    dump("st2", s2);
+    Img cat_s3{alloc((1024 + 6 * 384LL) * 625), 1024 + 6 * 384, 25, 25};
+    conv(s2, "st3.ds", 2, 1, kActNone, cat_s3.d);  // dw -> 25, 1024
+    hg_block(cat_s3, 1024, "st3.b0", true, 384, &s3, nullptr, nullptr);  // 25, 2048
+    dump("st3", s3);
+
+    // ---- hybrid encoder (:674-729)
+    Img cat8{alloc(512LL * 10000), 512, 100, 100}, cat16{alloc(512LL * 2500), 512, 50, 50};
+    Img catp16{alloc(512LL * 2500), 512, 50, 50}, catp32{alloc(512LL * 625), 512, 25, 25};
+    conv(s1, "enc_in0", 1, 0, kActNone, cat8.d + 256LL * 10000);  // p8 -> fpn1 concat slice 1
+    conv(s2, "enc_in1", 1, 0, kActNone, cat16.d + 256LL * 2500);  // p16 -> fpn0 concat slice 1
+    Img p32 = conv(s3, "enc_in2", 1, 0, kActNone);                 // 25, 256
+    {
+        // AIFI (:683-696): to_seq, qk = s + pos, post-norm MHA and FFN
+        Seq s{alloc(625LL * kDM), 625, kDM, kDM};
+        const Img pi = p32;
+        node("aifi.to_seq", 1, [=](hipStream_t st) { return ok(transpose(pi.d, s.d, kDM, 625, kDM, st)); });
+        Seq qk{alloc(625LL * kDM), 625, kDM, kDM};
+        node("aifi.pos", 1, [=](hipStream_t st) { return ok(add(s.d, pos_, qk.d, 625LL * kDM, st)); });
+        Seq at = mha(qk, s, "aifi", nullptr, nullptr);
+        Seq s1n = ln(at, s.d, "aifi.ln1");
+        Seq ff = lin(lin(s1n, "aifi.fc1", kActGelu), "aifi.fc2", kActNone);
+        Seq back = ln(ff, s1n.d, "aifi.ln2", nullptr, 1);  // channel-major == (25,25,256) image
+        p32.d = back.d;
+    }
+    dump("aifi", p32);
+    Img lat0 = conv(p32, "lat0", 1, 0, kActSilu, catp32.d + 256LL * 625);  // also pan1's concat slice 1
+    node("up0", 1, [=](hipStream_t st) { return ok(interp(lat0.d, nullptr, cat16.d, 256, 25, 25, 50, 50, 0, st)); });
+    Img f16 = csp(cat16, "fpn0", nullptr);
+    Img lat1 = conv(f16, "lat1", 1, 0, kActSilu, catp16.d + 256LL * 2500);  // also pan0's concat slice 1
+    node("up1", 1, [=](hipStream_t st) { return ok(interp(lat1.d, nullptr, cat8.d, 256, 50, 50, 100, 100, 0, st)); });
+    Img f8 = csp(cat8, "fpn1", nullptr);
+    dump("f8", f8);
+    conv(f8, "pand0", 2, 1, kActSilu, catp16.d);
+    Img n16 = csp(catp16, "pan0", nullptr);
+    dump("n16", n16);
+    conv(n16, "pand1", 2, 1, kActSilu, catp32.d);
+    Img n32 = csp(catp32, "pan1", nullptr);
+    dump("n32", n32);
+
+    // mask feature head (:711-724)
+    Img h0 = conv(f8, "mh0.0", 1, 1, kActSilu);  // 100, 64
+    Img h1 = conv(n16, "mh1.0", 1, 1, kActSilu);
+    Img m1{alloc(64LL * 10000), 64, 100, 100};
+    node("mh1.up", 1, [=](hipStream_t st) { return ok(interp(h1.d, h0.d, m1.d, 64, 50, 50, 100, 100, 1, st)); });
+    Img h2 = conv(n32, "mh2.0", 1, 1, kActSilu);
+    Img h2u{alloc(64LL * 2500), 64, 50, 50};
+    node("mh2.up", 1, [=](hipStream_t st) { return ok(interp(h2.d, nullptr, h2u.d, 64, 25, 25, 50, 50, 1, st)); });
+    Img h2b = conv(h2u, "mh2.2", 1, 1, kActSilu);
+    Img mf{alloc(64LL * 10000), 64, 100, 100};
+    node("mh2.up2", 1, [=](hipStream_t st) { return ok(interp(h2b.d, m1.d, mf.d, 64, 50, 50, 100, 100, 1, st)); });
+    Img mo = conv(mf, "mh.out", 1, 1, kActSilu);
+    Img ml = conv(s0, "mlat", 1, 1, kActSilu);  // 200, 64
+    Img mu{alloc(64LL * 40000), 64, 200, 200};
+    node("mh.up", 1, [=](hipStream_t st) { return ok(interp(mo.d, ml.d, mu.d, 64, 100, 100, 200, 200, 1, st)); });
+    Img mb = conv(mu, "mout.base", 1, 1, kActSilu);
+    Img mask_feat = conv(mb, "mout.conv", 1, 0, kActNone);  // 200, 32
+    dump("mask_feat", mask_feat);
+
+    // ---- decoder inputs (:791-801): 1x1 projections written token-major
+    // into one (13125, 256) source, level after level
+    Seq source{alloc((int64_t)NTOK * kDM), NTOK, kDM, kDM};
+    {
+        const Img lv[3] = {f8, n16, n32};
+        const int start[3] = {0, 10000, 12500};
+        for (int l = 0; l < 3; l++) {
+            const std::string nm = "dec_in" + std::to_string(l);
+            const int P = lv[l].H * lv[l].W;
+            GemmArgs g{};
+            g.A = W(nm + ".wr");
+            g.lda = kDM;
+            g.B = lv[l].d;
+            g.ldb = P;
+            g.C = source.d + (int64_t)start[l] * kDM;
+            g.ldc = kDM;
+            g.c_trans = 1;
+            g.bias = W(nm + ".bias");
+            g.M = kDM;
+            g.N = P;
+            g.K = lv[l].C;
+            g.batch = 1;
+            gemm(nm, g);
+        }
+    }
+    dump("source", source.d, {kDM, NTOK});
+    Seq memory{alloc((int64_t)NTOK * kDM), NTOK, kDM, kDM};
+    node("memory", 1, [=](hipStream_t st) { return ok(mul_rows(source.d, valid_, memory.d, NTOK, kDM, st)); });
+    Seq om = ln(lin(memory, "enc_out.l", kActNone), nullptr, "enc_out.ln");
+    Seq ecls = lin(om, "score_head", kActNone);  // (13125, 25)
+    topk_ = (int32_t *)alloc(NQ);
+    tagged("topk300", PPDL_OP_TOPK, 0, 0, view(topk_, {NQ}, PPDL_TYPE_I32), {view(ecls.d, {NC, NTOK})});
+    dump("topk_idx", topk_, {NQ}, true);
+    Seq target{alloc((int64_t)NQ * kDM), NQ, kDM, kDM};
+    node("target", 1, [=](hipStream_t st) { return ok(get_rows(om.d, topk_, target.d, NQ, st)); });
+    dump("target", target.d, {kDM, NQ});
+
+    // enhanced reference from the encoder masks (:808-822)
+    auto masks_of = [&](const Seq &mq, float *out, const char *nm) {
+        GemmArgs g{};
+        g.A = mq.d;
+        g.lda = mq.ld;
+        g.a_rowmajor = 1;
+        g.B = mask_feat.d;
+        g.ldb = NPIX;
+        g.C = out;
+        g.ldc = NPIX;
+        g.M = NQ;
+        g.N = NPIX;
+        g.K = 32;
+        g.batch = 1;
+        gemm(nm, g);
+    };
+    Seq outq0 = ln(target, nullptr, "dec_norm");
+    Seq mq0 = mlp3(outq0, "mq");
+    float *encm = alloc((int64_t)NQ * NPIX);
+    masks_of(mq0, encm, "enc_masks");
+    dump("enc_masks", encm, {NPIX, NQ});
+    refu_ = alloc((int64_t)NQ * 4);
+    tagged("mask_box", PPDL_OP_MASKBOX, 0, 0, view(refu_, {4, NQ}), {view(encm, {NPIX, NQ})});
+    dump("init_ref_unact", refu_, {4, NQ});
+    boxes_ = alloc((int64_t)NQ * 4);
+    node("ref0", 1, [=](hipStream_t st) {
+        hipError_t e = hipMemcpyAsync(boxes_, refu_, NQ * 4 * sizeof(float), hipMemcpyDeviceToDevice, st);
+        return e == hipSuccess ? ok(box_update(nullptr, boxes_, NQ * 4, st)) : 3;
+    });
+
+    // ---- decoder layers (:824-863)
+    Seq ref{boxes_, NQ, 4, 4};
+    Seq xq = target;
+    for (int i = 0; i < 6; i++) {
+        const std::string dp = "dec" + std::to_string(i);
+        Seq qpos = lin(lin(ref, "qpos.0", kActRelu), "qpos.1", kActNone);
+        Seq qk{alloc((int64_t)NQ * kDM), NQ, kDM, kDM};
+        const Seq xi = xq;
+        node(dp + ".qk", 1, [=](hipStream_t st) { return ok(add(xi.d, qpos.d, qk.d, (int64_t)NQ * kDM, st)); });
+        Seq sa = mha(qk, xq, dp + ".sa", nullptr, xq.d);  // x + attn
+        xq = ln(sa, nullptr, dp + ".ln1");
+        Seq z{alloc((int64_t)NQ * kDM), NQ, kDM, kDM};
+        const Seq x1 = xq;
+        node(dp + ".z", 1, [=](hipStream_t st) { return ok(add(x1.d, qpos.d, z.d, (int64_t)NQ * kDM, st)); });
+        Seq value = lin(source, dp + ".ca.vp", kActNone);
+        Seq offs = lin(z, dp + ".ca.so", kActNone);
+        Seq aw = lin(z, dp + ".ca.aw", kActNone);
+        Seq ca{alloc((int64_t)NQ * kDM), NQ, kDM, kDM};
+        tagged(dp + ".msdeform", PPDL_OP_MSDEF, 0, 0, view(ca.d, {kDM, NQ}),
+               {view(value.d, {kDM, NTOK}), view(offs.d, {192, NQ}), view(aw.d, {96, NQ}), view(ref.d, {4, NQ})});
+        Seq cao = lin(ca, dp + ".ca.op", kActNone, nullptr, xq.d, 2);  // x + ca
+        xq = ln(cao, nullptr, dp + ".ln2");
+        Seq ff = lin(lin(xq, dp + ".fc1", kActRelu), dp + ".fc2", kActNone, nullptr, xq.d, 2);
+        xq = ln(ff, nullptr, dp + ".ln3");
+        static const char *hn[6] = {"hidden0", "hidden1", "hidden2", "hidden3", "hidden4", "hidden5"};
+        dump(hn[i], xq.d, {kDM, NQ});
+        Seq delta = mlp3(xq, "bbox_head");
+        node(dp + ".ref", 1, [=](hipStream_t st) { return ok(box_update(delta.d, boxes_, NQ * 4, st)); });
+    }
+
+    // ---- heads (:865-876)
+    Seq outq = ln(xq, nullptr, "dec_norm");
+    Seq lg = lin(outq, "score_head", kActNone);
+    logits_ = lg.d;
+    Seq mq6 = mlp3(outq, "mq");
+    masks_ = alloc((int64_t)NQ * NPIX);
+    masks_of(mq6, masks_, "masks");
+    Seq gp = lin(lin(xq, "order5", kActNone), "gp", kActNone);  // (300, 128)
+    order_ = alloc((int64_t)NQ * NQ);
+    node("order", 1, [=](hipStream_t st) { return ok(order_logits(gp.d, order_, NQ, 64, 1.0f / 8.0f, st)); });
+
+    if (!missing_.empty()) {
+        *err = "missing tensor: " + missing_;
+        return false;
+    }
+    if (!bad_node_.empty()) {
+        *err = "node rejected by the op contract: " + bad_node_;
+        return false;
+    }
+    wg_dt_ = alloc(wg_need_);
+    wg_yt_ = alloc(wg_need_);
+    ws_bytes_ = (ws_need_ + 255) / 256 * 256;
+    ws_ = ws_bytes_ ? alloc(ws_bytes_ / 4) : nullptr;
+    if (oom_) {
+        *err = "device allocation failed while building the graph";
+        return false;
+    }
+
+    // host constants (:887-923)
+    std::vector<float> pos(625 * kDM), vm(NTOK);
+    double omega[64];
+    for (int i = 0; i < 64; i++) omega[i] = 1.0 / std::pow(10000.0, (double)i / 64.0);
+    for (int hh = 0; hh < 25; hh++)
+        for (int ww = 0; ww < 25; ww++) {
+            float *pp = pos.data() + (size_t)(hh * 25 + ww) * kDM;
+            for (int i = 0; i < 64; i++) {
+                pp[i] = (float)std::sin(hh * omega[i]);
+                pp[64 + i] = (float)std::cos(hh * omega[i]);
+                pp[128 + i] = (float)std::sin(ww * omega[i]);
+                pp[192 + i] = (float)std::cos(ww * omega[i]);
+            }
+        }
+    {
+        const int lw[3] = {100, 50, 25};
+        const float eps = 1e-2f;
+        int t2 = 0;
+        for (int l = 0; l < 3; l++) {
+            const float wh = 0.05f * (float)std::pow(2.0f, (float)l);
+            for (int yy = 0; yy < lw[l]; yy++)
+                for (int xx = 0; xx < lw[l]; xx++) {
+                    const float cx = ((float)xx + 0.5f) / (float)lw[l], cy = ((float)yy + 0.5f) / (float)lw[l];
+                    const bool okv = cx > eps && cx < 1.0f - eps && cy > eps && cy < 1.0f - eps && wh > eps &&
+                                     wh < 1.0f - eps;
+                    vm[t2++] = okv ? 1.0f : 0.0f;
+                }
+        }
+    }
+    if (hipMemcpy(pos_, pos.data(), pos.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(valid_, vm.data(), vm.size() * 4, hipMemcpyHostToDevice) != hipSuccess) {
+        *err = "upload of host constants failed";
+        return false;
+    }
+    return true;
+}
+
+// One eager pass (every node validated and launched), then stream capture of
+// the same sequence into a hipGraph.
+bool Net::capture(std::string *err) {
+    std::vector<float> zero(3LL * IMG * IMG, 0.0f);
+    if (!upload_image(zero.data())) {
+        *err = "image upload failed";
+        return false;
+    }
+    for (auto &n : nodes_) {
+        const int rc = n.run(stream_);
+        if (rc != 0) {
+            *err = "node " + n.name + " failed (" + std::to_string(rc) + ")";
+            return false;
+        }
+    }
+    if (hipStreamSynchronize(stream_) != hipSuccess) {
+        *err = "eager pass failed";
+        return false;
+    }
+    if (hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal) != hipSuccess) {
+        *err = "hipStreamBeginCapture failed";
+        return false;
+    }
+    int rc = 0;
+    for (auto &n : nodes_)
+        if (!rc) rc = n.run(stream_);
+    hipGraph_t g = nullptr;
+    const hipError_t e = hipStreamEndCapture(stream_, &g);
+    if (rc || e != hipSuccess || !g) {
+        if (g) (void)hipGraphDestroy(g);
+        *err = "graph capture failed";
+        return false;
+    }
+    graph_ = g;
+    if (hipGraphInstantiate(&exec_, graph_, nullptr, nullptr, 0) != hipSuccess) {
+        *err = "hipGraphInstantiate failed";
+        return false;
+    }
+    return true;
+}
+
+bool Net::upload_image(const float *host) {
+    return hipMemcpyAsync(image_, host, 3LL * IMG * IMG * 4, hipMemcpyHostToDevice, stream_) == hipSuccess &&
+           hipStreamSynchronize(stream_) == hipSuccess;
+}
+
+int Net::replay() {
+    if (hipGraphLaunch(exec_, stream_) != hipSuccess) return 2;
+    return hipStreamSynchronize(stream_) == hipSuccess ? 0 : 2;
+}
+
+double Net::time_graph(int iters) {
+    hipEvent_t e0, e1;
+    if (iters < 1 || hipEventCreate(&e0) != hipSuccess) return -1.0;
+    if (hipEventCreate(&e1) != hipSuccess) {
+        (void)hipEventDestroy(e0);
+        return -1.0;
+    }
+    bool good = hipEventRecord(e0, stream_) == hipSuccess;
+    for (int i = 0; good && i < iters; i++) good = hipGraphLaunch(exec_, stream_) == hipSuccess;
+    good = good && hipEventRecord(e1, stream_) == hipSuccess && hipEventSynchronize(e1) == hipSuccess;
+    float ms = 0.0f;
+    good = good && hipEventElapsedTime(&ms, e0, e1) == hipSuccess;
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    return good ? (double)ms / iters : -1.0;
+}
+
+// ---------------------------------------------------------------------------
+// Postprocess (src/ppdoclayout.cpp:927-993), on the host: reading-order votes,
+// top-300 over the 7500 class scores, box restore to the original size, mask
+// binarisation.
+void postprocess(const std::vector<float> &logits, const std::vector<float> &boxes, const std::vector<float> &order,
+                 const std::vector<float> &maskl, int ori_h, int ori_w, std::vector<float> &out0,
+                 std::vector<int32_t> &out2, std::vector<int32_t> &sel) {
+    std::vector<float> votes(NQ, 0.0f);
+    for (int j = 0; j < NQ; j++) {
+        float acc = 0.0f;
+        for (int i = 0; i < NQ; i++) {
+            if (i == j) continue;
+            const float diff = order[(size_t)j + (size_t)NQ * i] - order[(size_t)i + (size_t)NQ * j];
+            acc += 1.0f / (1.0f + std::exp(-diff));
+        }
+        votes[j] = acc;
+    }
+    std::vector<int> rank_of(NQ);
+    std::iota(rank_of.begin(), rank_of.end(), 0);
+    std::stable_sort(rank_of.begin(), rank_of.end(), [&](int a2, int b2) { return votes[a2] < votes[b2]; });
+    std::vector<int> order_seq(NQ);
+    for (int r = 0; r < NQ; r++) order_seq[rank_of[r]] = r;
+
+    std::vector<float> scores((size_t)NQ * NC);
+    for (size_t i = 0; i < scores.size(); i++) scores[i] = 1.0f / (1.0f + std::exp(-logits[i]));
+    std::vector<int> flat(scores.size());
+    std::iota(flat.begin(), flat.end(), 0);
+    std::partial_sort(flat.begin(), flat.begin() + NQ, flat.end(), [&](int a2, int b2) {
+        if (scores[a2] != scores[b2]) return scores[a2] > scores[b2];
+        return a2 < b2;
+    });
+    const float sf_h = (float)IMG / (float)ori_h, sf_w = (float)IMG / (float)ori_w;
+    const float oh = std::floor((float)IMG / sf_h + 0.5f), ow = std::floor((float)IMG / sf_w + 0.5f);
+    out0.assign((size_t)NQ * 7, 0.0f);
+    out2.assign((size_t)NQ * NPIX, 0);
+    sel.assign(NQ, 0);
+    for (int r = 0; r < NQ; r++) {
+        const int f = flat[r], q = f / NC, c = f % NC;
+        sel[r] = f;
+        const float *b = boxes.data() + (size_t)q * 4;
+        float *o = out0.data() + (size_t)r * 7;
+        o[0] = (float)c;
+        o[1] = scores[f];
+        o[2] = (b[0] - b[2] * 0.5f) * ow;
+        o[3] = (b[1] - b[3] * 0.5f) * oh;
+        o[4] = (b[0] + b[2] * 0.5f) * ow;
+        o[5] = (b[1] + b[3] * 0.5f) * oh;
+        o[6] = (float)order_seq[q];
+        const float *m = maskl.data() + (size_t)q * NPIX;
+        int32_t *mo = out2.data() + (size_t)r * NPIX;
+        for (int p = 0; p < NPIX; p++) mo[p] = m[p] > 0.0f ? 1 : 0;
+    }
+}
+
+bool write_file(const std::string &path, const void *src, size_t nbytes) {
+    FILE *f = fopen(path.c_str(), "wb");
+    if (!f) return false;
+    const size_t n = fwrite(src, 1, nbytes, f);
+    fclose(f);
+    return n == nbytes;
+}
+
+}  // namespace
+}  // namespace ppdl
+
+struct ppdl_ctx {
+    std::unique_ptr<ppdl::Net> net;
+    bool computed = false;
+    std::vector<float> out0, raw_logits, raw_boxes, raw_order, raw_masks;
+    std::vector<int32_t> out2, raw_sel;
+};
+
+namespace {
+bool fetch(ppdl_ctx *c) {
+    using namespace ppdl;
+    c->raw_logits.resize((size_t)NQ * NC);
+    c->raw_boxes.resize((size_t)NQ * 4);
+    c->raw_order.resize((size_t)NQ * NQ);
+    c->raw_masks.resize((size_t)NQ * NPIX);
+    return hipMemcpy(c->raw_logits.data(), c->net->logits_, c->raw_logits.size() * 4, hipMemcpyDeviceToHost) ==
+               hipSuccess &&
+           hipMemcpy(c->raw_boxes.data(), c->net->boxes_, c->raw_boxes.size() * 4, hipMemcpyDeviceToHost) ==
+               hipSuccess &&
+           hipMemcpy(c->raw_order.data(), c->net->order_, c->raw_order.size() * 4, hipMemcpyDeviceToHost) ==
+               hipSuccess &&
+           hipMemcpy(c->raw_masks.data(), c->net->masks_, c->raw_masks.size() * 4, hipMemcpyDeviceToHost) ==
+               hipSuccess;
+}
+}  // namespace
+
+extern "C" PPDL_API ppdl_ctx *ppdl_init_ex(const char *model_path, int backend, int enable_dumps) {
+    if (!model_path) return nullptr;
+    if (backend == PPDL_BACKEND_CPU) {
+        fprintf(stderr, "ppdl: this build has no CPU backend; use PPDL_BACKEND_HIP\n");
+        return nullptr;
+    }
+    if (backend != PPDL_BACKEND_CUDA && backend != PPDL_BACKEND_HIP) return nullptr;
+    {
+        // the file is checked before any device work, so a bad path or a
+        // malformed file fails the same way on every host
+        ppdl::GgufFile g;
+        std::string err;
+        if (!ppdl::gguf_open(model_path, &g, &err)) {
+            fprintf(stderr, "ppdl: %s\n", err.c_str());
+            return nullptr;
+        }
+    }
+    int ndev = 0;
+    if (hipGetDeviceCount(&ndev) != hipSuccess || ndev < 1) {
+        fprintf(stderr, "ppdl: no GPU backend available\n");
+        return nullptr;
+    }
+    auto *c = new ppdl_ctx();
+    c->net.reset(new ppdl::Net());
+    std::string err;
+    if (!c->net->load(model_path, &err) || !c->net->build(enable_dumps != 0, &err) || !c->net->capture(&err)) {
+        fprintf(stderr, "ppdl: %s\n", err.c_str());
+        delete c;
+        return nullptr;
+    }
+    fprintf(stderr, "ppdl: loaded %s; graph of %d kernel launches\n", model_path, c->net->nodes());
+    return c;
+}
+
+extern "C" PPDL_API ppdl_ctx *ppdl_init(const char *model_path, int backend) {
+    return ppdl_init_ex(model_path, backend, 0);
+}
+
+extern "C" PPDL_API int ppdl_compute(ppdl_ctx *c, const float *image_chw) {
+    if (!c || !image_chw) return 1;
+    if (!c->net->upload_image(image_chw)) return 2;
+    const int rc = c->net->replay();
+    if (rc == 0) c->computed = true;
+    return rc;
+}
+
+extern "C" PPDL_API int ppdl_infer(ppdl_ctx *c, const float *image_chw, int ori_h, int ori_w, ppdl_result *res) {
+    if (!c || !image_chw || !res || ori_h <= 0 || ori_w <= 0) return 1;
+    if (!c->net->upload_image(image_chw)) return 2;
+    const auto t0 = std::chrono::steady_clock::now();
+    if (c->net->replay() != 0) {
+        fprintf(stderr, "ppdl: graph compute failed\n");
+        return 2;
+    }
+    const auto t1 = std::chrono::steady_clock::now();
+    c->computed = true;
+    if (!fetch(c)) return 2;
+    ppdl::postprocess(c->raw_logits, c->raw_boxes, c->raw_order, c->raw_masks, ori_h, ori_w, c->out0, c->out2,
+                      c->raw_sel);
+    res->dets = c->out0.data();
+    res->num_dets = ppdl::NQ;
+    res->masks = c->out2.data();
+    res->infer_ms = std::chrono::duration<double, std::milli>(t1 - t0).count();
+    return 0;
+}
+
+extern "C" PPDL_API int ppdl_dump(ppdl_ctx *c, const char *dir) {
+    if (!c || !dir) return 1;
+    if (c->net->dumps_.empty()) {
+        fprintf(stderr, "ppdl: dumps not enabled\n");
+        return 1;
+    }
+    if (!c->computed) {
+        fprintf(stderr, "ppdl: no inference to dump\n");
+        return 1;
+    }
+    mkdir(dir, 0755);
+    FILE *mf = fopen((std::string(dir) + "/shapes.txt").c_str(), "w");
+    if (!mf) return 1;
+    for (const auto &d : c->net->dumps_) {
+        int64_t n = 1;
+        for (int64_t e : d.ne) n *= e;
+        std::vector<uint8_t> buf((size_t)n * 4);
+        if (hipMemcpy(buf.data(), d.d, buf.size(), hipMemcpyDeviceToHost) != hipSuccess) {
+            fclose(mf);
+            return 1;
+        }
+        ppdl::write_file(std::string(dir) + "/" + d.name + ".bin", buf.data(), buf.size());
+        std::vector<int64_t> ne = d.ne;
+        while (ne.size() < 4) ne.push_back(1);
+        fprintf(mf, "%s %s %lld %lld %lld %lld\n", d.name.c_str(), d.i32 ? "i32" : "f32", (long long)ne[0],
+                (long long)ne[1], (long long)ne[2], (long long)ne[3]);
+    }
+    fclose(mf);
+    return 0;
+}
+
+extern "C" PPDL_API int ppdl_dump_raw(ppdl_ctx *c, const char *pfx) {
+    if (!c || !pfx) return 1;
+    if (!c->computed || c->raw_logits.empty()) {
+        fprintf(stderr, "ppdl: no inference to dump\n");
+        return 1;
+    }
+    const std::string p(pfx);
+    bool good = ppdl::write_file(p + "logits.bin", c->raw_logits.data(), c->raw_logits.size() * 4);
+    good = ppdl::write_file(p + "boxes.bin", c->raw_boxes.data(), c->raw_boxes.size() * 4) && good;
+    good = ppdl::write_file(p + "order.bin", c->raw_order.data(), c->raw_order.size() * 4) && good;
+    good = ppdl::write_file(p + "sel.bin", c->raw_sel.data(), c->raw_sel.size() * 4) && good;
+    return good ? 0 : 1;
+}
+
+extern "C" PPDL_API void ppdl_free(ppdl_ctx *c) { delete c; }
+
+extern "C" PPDL_API int64_t ppdl_get_raw(ppdl_ctx *c, int which, void *dst, int64_t n) {
+    using namespace ppdl;
+    if (!c || !dst || !c->computed) return -1;
+    const void *src = nullptr;
+    int64_t cnt = 0;
+    switch (which) {
+        case 0: src = c->net->logits_; cnt = (int64_t)NQ * NC; break;
+        case 1: src = c->net->boxes_; cnt = (int64_t)NQ * 4; break;
+        case 2: src = c->net->order_; cnt = (int64_t)NQ * NQ; break;
+        case 3: src = c->net->masks_; cnt = (int64_t)NQ * NPIX; break;
+        case 4: src = c->net->topk_; cnt = NQ; break;
+        case 5: src = c->net->refu_; cnt = (int64_t)NQ * 4; break;
+        default: return -1;
+    }
+    if (n < cnt) return -1;
+    return hipMemcpy(dst, src, (size_t)cnt * 4, hipMemcpyDeviceToHost) == hipSuccess ? cnt : -1;
+}
+
+extern "C" PPDL_API double ppdl_time_graph(ppdl_ctx *c, int iters) {
+    if (!c) return -1.0;
+    return c->net->time_graph(iters);
+}
+
+extern "C" PPDL_API int ppdl_graph_nodes(ppdl_ctx *c) { return c ? c->net->nodes() : 0; }

@@ -1,0 +1,361 @@
+// Stock ops of the PP-DocLayoutV3 graph that are not tagged ops: the work the
+// reference leaves to ggml's own kernels (depthwise conv, pooling,
+// interpolation, layer norm, attention, elementwise), written for gfx950.
+// Semantics follow the ggml ops the reference graph calls
+// (src/ppdoclayout.cpp:363-883); each kernel cites its call site.
+#include "net_internal.h"
+
+#pragma clang fp contract(off)
+
+namespace ppdl {
+namespace {
+
+__device__ __forceinline__ float act_f(float v, int act) {
+    if (act == kActRelu) return v > 0.0f ? v : 0.0f;
+    if (act == kActSilu) return v / (1.0f + expf(-v));
+    if (act == kActGelu) return 0.5f * v * (1.0f + erff(v * 0.70710678118654752f));
+    if (act == kActSigmoid) return 1.0f / (1.0f + expf(-v));
+    return v;
+}
+
+// ---------------------------------------------------------------------------
+// Depthwise conv + bias + act (ggml_conv_2d_dw_direct + add + act,
+// src/ppdoclayout.cpp:400-404).  One thread per output pixel, taps summed in
+// (kh, kw) order.  w: [C][K][K].
+__global__ __launch_bounds__(256) void k_dwconv(const float *__restrict__ x, const float *__restrict__ w,
+                                                const float *__restrict__ b, float *__restrict__ out, int C,
+                                                int IH, int IW, int OH, int OW, int K, int S, int P, int act) {
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t total = (int64_t)C * OH * OW;
+    if (idx >= total) return;
+    const int c = (int)(idx / ((int64_t)OH * OW));
+    const int rem = (int)(idx - (int64_t)c * OH * OW);
+    const int oy = rem / OW, ox = rem - oy * OW;
+    const float *xc = x + (int64_t)c * IH * IW;
+    const float *wc = w + (int64_t)c * K * K;
+    float s = 0.0f;
+    for (int kh = 0; kh < K; kh++) {
+        const int iy = oy * S + kh - P;
+        if (iy < 0 || iy >= IH) continue;
+        for (int kw = 0; kw < K; kw++) {
+            const int ix = ox * S + kw - P;
+            if (ix < 0 || ix >= IW) continue;
+            s = fmaf(xc[(int64_t)iy * IW + ix], wc[kh * K + kw], s);
+        }
+    }
+    out[idx] = act_f(s + b[c], act);
+}
+
+// 2x2 stride-1 max pool of x zero-padded by one column and one row at the
+// right/bottom (ggml_pad + ggml_pool_2d, src/ppdoclayout.cpp:621-626): the
+// output keeps x's size.
+__global__ __launch_bounds__(256) void k_maxpool2_padend(const float *__restrict__ x, float *__restrict__ out,
+                                                         int C, int H, int W) {
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= (int64_t)C * H * W) return;
+    const int c = (int)(idx / ((int64_t)H * W));
+    const int rem = (int)(idx - (int64_t)c * H * W);
+    const int y = rem / W, xx = rem - y * W;
+    const float *xc = x + (int64_t)c * H * W;
+    const float v00 = xc[(int64_t)y * W + xx];
+    const float v01 = xx + 1 < W ? xc[(int64_t)y * W + xx + 1] : 0.0f;
+    const float v10 = y + 1 < H ? xc[(int64_t)(y + 1) * W + xx] : 0.0f;
+    const float v11 = (xx + 1 < W && y + 1 < H) ? xc[(int64_t)(y + 1) * W + xx + 1] : 0.0f;
+    out[idx] = fmaxf(fmaxf(v00, v01), fmaxf(v10, v11));
+}
+
+// Interpolation (ggml_interpolate, src/ppdoclayout.cpp:670-672): nearest
+// (src = floor(dst * in / out)) or bilinear with half-pixel centres and
+// edge clamping; out = interp(x) + add (add may be null).
+__global__ __launch_bounds__(256) void k_interp(const float *__restrict__ x, const float *__restrict__ add,
+                                                float *__restrict__ out, int C, int IH, int IW, int OH, int OW,
+                                                int bilinear) {
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= (int64_t)C * OH * OW) return;
+    const int c = (int)(idx / ((int64_t)OH * OW));
+    const int rem = (int)(idx - (int64_t)c * OH * OW);
+    const int oy = rem / OW, ox = rem - oy * OW;
+    const float *xc = x + (int64_t)c * IH * IW;
+    float v;
+    if (!bilinear) {
+        const int iy = (int)((int64_t)oy * IH / OH), ix = (int)((int64_t)ox * IW / OW);
+        v = xc[(int64_t)iy * IW + ix];
+    } else {
+        const float sy = (float)OH / (float)IH, sx = (float)OW / (float)IW;
+        const float fy = ((float)oy + 0.5f) / sy - 0.5f, fx = ((float)ox + 0.5f) / sx - 0.5f;
+        const float fly = floorf(fy), flx = floorf(fx);
+        int y0 = (int)fly, x0 = (int)flx;
+        int y1 = y0 + 1, x1 = x0 + 1;
+        y0 = max(0, min(y0, IH - 1));
+        y1 = max(0, min(y1, IH - 1));
+        x0 = max(0, min(x0, IW - 1));
+        x1 = max(0, min(x1, IW - 1));
+        const float dy = fmaxf(0.0f, fminf(fy - fly, 1.0f)), dx = fmaxf(0.0f, fminf(fx - flx, 1.0f));
+        const float a = xc[(int64_t)y0 * IW + x0], bb = xc[(int64_t)y0 * IW + x1];
+        const float cc = xc[(int64_t)y1 * IW + x0], d = xc[(int64_t)y1 * IW + x1];
+        v = a * (1.0f - dx) * (1.0f - dy) + bb * dx * (1.0f - dy) + cc * (1.0f - dx) * dy + d * dx * dy;
+    }
+    if (add) v += add[idx];
+    out[idx] = v;
+}
+
+// ---------------------------------------------------------------------------
+// Layer norm over the 256 features of each token (ggml_norm eps 1e-5, then
+// * gamma + beta, src/ppdoclayout.cpp:550-554), with the residual sum of
+// the reference's ln(x + y) fused: out = LN(a + b).  One wave per token,
+// 4 features per lane; mean and variance by wave reductions.  out_chw
+// stores the result channel-major ([256][T]) instead of token-major.
+__global__ __launch_bounds__(256) void k_layernorm(const float *__restrict__ a, const float *__restrict__ b,
+                                                   const float *__restrict__ gamma,
+                                                   const float *__restrict__ beta, float *__restrict__ out,
+                                                   int T, float eps, int out_chw) {
+    const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (t >= T) return;
+    const float4 av = *reinterpret_cast<const float4 *>(a + (int64_t)t * kDM + lane * 4);
+    float v[4] = {av.x, av.y, av.z, av.w};
+    if (b) {
+        const float4 bv = *reinterpret_cast<const float4 *>(b + (int64_t)t * kDM + lane * 4);
+        v[0] += bv.x;
+        v[1] += bv.y;
+        v[2] += bv.z;
+        v[3] += bv.w;
+    }
+    float s = (v[0] + v[1]) + (v[2] + v[3]);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
+    const float mean = s / (float)kDM;
+    float q = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        v[i] -= mean;
+        q += v[i] * v[i];
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) q += __shfl_xor(q, o);
+    const float scale = 1.0f / sqrtf(q / (float)kDM + eps);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int c = lane * 4 + i;
+        const float y = v[i] * scale * gamma[c] + beta[c];
+        if (out_chw)
+            out[(int64_t)c * T + t] = y;
+        else
+            out[(int64_t)t * kDM + c] = y;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Multi-head attention core (src/ppdoclayout.cpp:572-587): per head h,
+// out[t][h*32+c] = sum_s softmax_s(q_t . k_s / sqrt(32)) v[s][h*32+c].
+// q, k, v are token-major with row strides ldq/ldk/ldv.  A block owns one
+// head and 64 queries; 4 threads per query each cover a quarter of the keys
+// with an online softmax, then merge.  Keys/values stream through LDS in
+// chunks of 64.
+constexpr int kAttQ = 64, kAttKC = 64;
+
+__global__ __launch_bounds__(256) void k_attention(const float *__restrict__ q, int ldq,
+                                                   const float *__restrict__ k, int ldk,
+                                                   const float *__restrict__ v, int ldv, float *__restrict__ out,
+                                                   int ldo, int T, float scale) {
+    __shared__ float Ks[kAttKC][kHD + 1];
+    __shared__ float Vs[kAttKC][kHD + 1];
+    __shared__ float red_m[kAttQ][4], red_l[kAttQ][4];
+    __shared__ float red_o[kAttQ][4][kHD + 1];
+    const int h = blockIdx.y;
+    const int qi = threadIdx.x >> 2, part = threadIdx.x & 3;
+    const int t = blockIdx.x * kAttQ + qi;
+    const bool live = t < T;
+    float qv[kHD], acc[kHD];
+#pragma unroll
+    for (int c = 0; c < kHD; c++) {
+        qv[c] = live ? q[(int64_t)t * ldq + h * kHD + c] : 0.0f;
+        acc[c] = 0.0f;
+    }
+    float mx = -INFINITY, l = 0.0f;
+    for (int s0 = 0; s0 < T; s0 += kAttKC) {
+        __syncthreads();
+        for (int i = threadIdx.x; i < kAttKC * kHD; i += 256) {
+            const int r = i / kHD, c = i - r * kHD;
+            const int s = s0 + r;
+            Ks[r][c] = s < T ? k[(int64_t)s * ldk + h * kHD + c] : 0.0f;
+            Vs[r][c] = s < T ? v[(int64_t)s * ldv + h * kHD + c] : 0.0f;
+        }
+        __syncthreads();
+        const int n = min(kAttKC, T - s0);
+        for (int r = part; r < n; r += 4) {
+            float d = 0.0f;
+#pragma unroll
+            for (int c = 0; c < kHD; c++) d = fmaf(qv[c], Ks[r][c], d);
+            d *= scale;
+            if (d > mx) {
+                const float corr = expf(mx - d);
+                l *= corr;
+#pragma unroll
+                for (int c = 0; c < kHD; c++) acc[c] *= corr;
+                mx = d;
+            }
+            const float p = expf(d - mx);
+            l += p;
+#pragma unroll
+            for (int c = 0; c < kHD; c++) acc[c] = fmaf(p, Vs[r][c], acc[c]);
+        }
+    }
+    red_m[qi][part] = mx;
+    red_l[qi][part] = l;
+#pragma unroll
+    for (int c = 0; c < kHD; c++) red_o[qi][part][c] = acc[c];
+    __syncthreads();
+    if (part == 0 && live) {
+        float m = red_m[qi][0];
+        for (int p = 1; p < 4; p++) m = fmaxf(m, red_m[qi][p]);
+        float L = 0.0f, w[4];
+        for (int p = 0; p < 4; p++) {
+            w[p] = red_m[qi][p] == -INFINITY ? 0.0f : expf(red_m[qi][p] - m);
+            L += w[p] * red_l[qi][p];
+        }
+        for (int c = 0; c < kHD; c++) {
+            float o = 0.0f;
+            for (int p = 0; p < 4; p++) o += w[p] * red_o[qi][p][c];
+            out[(int64_t)t * ldo + h * kHD + c] = o / L;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Elementwise helpers.
+__global__ __launch_bounds__(256) void k_add(const float *__restrict__ a, const float *__restrict__ b,
+                                             float *__restrict__ out, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) out[i] = a[i] + b[i];
+}
+
+// out[t][c] = x[t][c] * mask[t]  (memory = source * valid, src/ppdoclayout.cpp:801)
+__global__ __launch_bounds__(256) void k_mul_rows(const float *__restrict__ x, const float *__restrict__ mask,
+                                                  float *__restrict__ out, int64_t T, int D) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < T * D) out[i] = x[i] * mask[i / D];
+}
+
+__device__ __forceinline__ float inv_sigmoid(float x) {
+    // src/ppdoclayout.cpp:589-594: clamp to [0,1], log(max(x,1e-5)) - log(max(1-x,1e-5))
+    x = fminf(fmaxf(x, 0.0f), 1.0f);
+    const float x1 = fminf(fmaxf(x, 1e-5f), 1.0f);
+    const float x2 = fminf(fmaxf(1.0f - x, 1e-5f), 1.0f);
+    return logf(x1) - logf(x2);
+}
+
+// Box refinement (src/ppdoclayout.cpp:860-862): ref = sigmoid(delta + inv_sigmoid(ref)).
+// With delta == null: ref = sigmoid(ref) (the initial reference).
+__global__ __launch_bounds__(256) void k_box_update(const float *__restrict__ delta, float *__restrict__ ref,
+                                                    int n) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    const float z = delta ? delta[i] + inv_sigmoid(ref[i]) : ref[i];
+    ref[i] = 1.0f / (1.0f + expf(-z));
+}
+
+// target = om[idx]: ggml_get_rows of 256-wide token rows (src/ppdoclayout.cpp:805)
+__global__ __launch_bounds__(256) void k_get_rows(const float *__restrict__ src, const int32_t *__restrict__ idx,
+                                                  float *__restrict__ out, int nrows) {
+    const int r = blockIdx.x, c = threadIdx.x;
+    if (r >= nrows) return;
+    out[(int64_t)r * kDM + c] = src[(int64_t)idx[r] * kDM + c];
+}
+
+// Reading-order logits (src/ppdoclayout.cpp:874-876):
+// order[m + NQ*n] = scale * sum_c gp[m][64 + c] * gp[n][c]  (ggml_mul_mat(kv, qv))
+__global__ __launch_bounds__(256) void k_order(const float *__restrict__ gp, float *__restrict__ out, int nq,
+                                               int hd, float scale) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (int64_t)nq * nq) return;
+    const int m = (int)(i % nq), n = (int)(i / nq);
+    const float *kv = gp + (int64_t)m * 2 * hd + hd, *qv = gp + (int64_t)n * 2 * hd;
+    float s = 0.0f;
+    for (int c = 0; c < hd; c++) s = fmaf(kv[c], qv[c], s);
+    out[i] = s * scale;
+}
+
+// CHW [C][P] -> token-major [P][C] (the reference's to_seq / cont(permute)),
+// through a 32x32 LDS tile.
+__global__ __launch_bounds__(256) void k_transpose(const float *__restrict__ in, float *__restrict__ out,
+                                                   int rows, int cols, int ldo) {
+    __shared__ float tile[32][33];
+    const int c0 = blockIdx.x * 32, r0 = blockIdx.y * 32;
+    const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+    for (int r = ty; r < 32; r += 8)
+        if (r0 + r < rows && c0 + tx < cols) tile[r][tx] = in[(int64_t)(r0 + r) * cols + c0 + tx];
+    __syncthreads();
+    for (int c = ty; c < 32; c += 8)
+        if (c0 + c < cols && r0 + tx < rows) out[(int64_t)(c0 + c) * ldo + r0 + tx] = tile[tx][c];
+}
+
+unsigned blocks_for(int64_t n) { return (unsigned)((n + 255) / 256); }
+
+}  // namespace
+
+hipError_t dwconv(const float *x, const float *w, const float *b, float *out, int C, int IH, int IW, int K, int S,
+                  int P, int act, hipStream_t s) {
+    const int OH = (IH + 2 * P - K) / S + 1, OW = (IW + 2 * P - K) / S + 1;
+    hipLaunchKernelGGL(k_dwconv, dim3(blocks_for((int64_t)C * OH * OW)), dim3(256), 0, s, x, w, b, out, C, IH,
+                       IW, OH, OW, K, S, P, act);
+    return hipGetLastError();
+}
+
+hipError_t maxpool2_padend(const float *x, float *out, int C, int H, int W, hipStream_t s) {
+    hipLaunchKernelGGL(k_maxpool2_padend, dim3(blocks_for((int64_t)C * H * W)), dim3(256), 0, s, x, out, C, H, W);
+    return hipGetLastError();
+}
+
+hipError_t interp(const float *x, const float *add, float *out, int C, int IH, int IW, int OH, int OW,
+                  int bilinear, hipStream_t s) {
+    hipLaunchKernelGGL(k_interp, dim3(blocks_for((int64_t)C * OH * OW)), dim3(256), 0, s, x, add, out, C, IH, IW,
+                       OH, OW, bilinear);
+    return hipGetLastError();
+}
+
+hipError_t layernorm(const float *a, const float *b, const float *gamma, const float *beta, float *out, int T,
+                     int out_chw, hipStream_t s) {
+    hipLaunchKernelGGL(k_layernorm, dim3((T + 3) / 4), dim3(256), 0, s, a, b, gamma, beta, out, T, 1e-5f, out_chw);
+    return hipGetLastError();
+}
+
+hipError_t attention(const float *q, int ldq, const float *k, int ldk, const float *v, int ldv, float *out,
+                     int ldo, int T, hipStream_t s) {
+    hipLaunchKernelGGL(k_attention, dim3((T + kAttQ - 1) / kAttQ, kNH), dim3(256), 0, s, q, ldq, k, ldk, v, ldv,
+                       out, ldo, T, 1.0f / sqrtf((float)kHD));
+    return hipGetLastError();
+}
+
+hipError_t add(const float *a, const float *b, float *out, int64_t n, hipStream_t s) {
+    hipLaunchKernelGGL(k_add, dim3(blocks_for(n)), dim3(256), 0, s, a, b, out, n);
+    return hipGetLastError();
+}
+
+hipError_t mul_rows(const float *x, const float *mask, float *out, int64_t T, int D, hipStream_t s) {
+    hipLaunchKernelGGL(k_mul_rows, dim3(blocks_for(T * D)), dim3(256), 0, s, x, mask, out, T, D);
+    return hipGetLastError();
+}
+
+hipError_t box_update(const float *delta, float *ref, int n, hipStream_t s) {
+    hipLaunchKernelGGL(k_box_update, dim3(blocks_for(n)), dim3(256), 0, s, delta, ref, n);
+    return hipGetLastError();
+}
+
+hipError_t get_rows(const float *src, const int32_t *idx, float *out, int nrows, hipStream_t s) {
+    hipLaunchKernelGGL(k_get_rows, dim3(nrows), dim3(kDM), 0, s, src, idx, out, nrows);
+    return hipGetLastError();
+}
+
+hipError_t order_logits(const float *gp, float *out, int nq, int hd, float scale, hipStream_t s) {
+    hipLaunchKernelGGL(k_order, dim3(blocks_for((int64_t)nq * nq)), dim3(256), 0, s, gp, out, nq, hd, scale);
+    return hipGetLastError();
+}
+
+hipError_t transpose(const float *in, float *out, int rows, int cols, int ldo, hipStream_t s) {
+    hipLaunchKernelGGL(k_transpose, dim3((cols + 31) / 32, (rows + 31) / 32), dim3(256), 0, s, in, out, rows, cols,
+                       ldo);
+    return hipGetLastError();
+}
+
+}  // namespace ppdl

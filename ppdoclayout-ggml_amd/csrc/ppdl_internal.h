@@ -44,9 +44,13 @@ constexpr double kG[6][3] = {
     {0.0, 0.0, 1.0},
 };
 
-// ---- GEMM core: C[m][n] = epi( sum_k At[k][m] * B[k][n] ) ----
-// A is stored k-major (element (m,k) at A[k*lda + m]); B is either a dense
-// k-major matrix or an implicit im2col view of a CHW image.
+// ---- GEMM core: C[m][n] = epi( sum_k A(m,k) * B(k,n) ) ----
+// A is stored k-major (element (m,k) at A[k*lda + m], a_rowmajor = 0) or
+// row-major (A[m*lda + k], a_rowmajor = 1: token-major activations); B is a
+// dense k-major matrix or an implicit im2col view of a CHW image.
+// Epilogue: v = acc + bias[m or n]; v += add (add_mode 1); v = act(v);
+// v += add (add_mode 2); store at C[m*ldc + n], or C[n*ldc + m] when
+// c_trans (a CHW conv result written token-major).  `add` uses C's layout.
 struct GemmArgs {
     const float *A;
     int64_t lda, sA;  // sA: batch stride (elements)
@@ -54,12 +58,18 @@ struct GemmArgs {
     int64_t ldb, sB;
     float *C;
     int64_t ldc, sC;
-    const float *bias;  // per-m bias or nullptr
+    const float *bias;  // per-m (bias_n = 0) or per-n (bias_n = 1) bias, or nullptr
     int M, N, K, batch, act;
-    // implicit im2col geometry: B[k][n] = x[ic][oy*S-P+kh][ox*S-P+kw],
-    // k = (kh*KW + kw)*IC + ic, n = oy*OW + ox
+    // implicit im2col geometry: B[k][n] = x[ic][oy*S-P+kh][ox*S-P+kw] with
+    // zeros outside [0,IH) x [0,IW) (the image may be padded beyond IH/IW by
+    // choosing OW/OH), k = (kh*KW + kw)*IC + ic, n = oy*OW + ox
     int IC, IH, IW, OW, KW, S, P;
+    int a_rowmajor, bias_n, c_trans, add_mode;
+    const float *add;
 };
+
+// act codes of the GEMM epilogue and the elementwise kernels
+enum { kActNone = 0, kActRelu = 1, kActSilu = 2, kActGelu = 3, kActSigmoid = 4 };
 
 // Split-K workspace: fp32 partials, splits x batch x M x N, fully rewritten by
 // every launch that uses it (no initial contents required).

@@ -49,12 +49,13 @@ int status_of(hipError_t e) { return e == hipSuccess ? PPDL_OK : PPDL_ELAUNCH; }
 
 constexpr int64_t kMaxI32 = 0x7fffffff;
 
-// Index of the optional split-K workspace src of a GEMM op, or -1.
-int ws_index(int op) {
-    switch (op) {
+// Index of the optional split-K workspace src of a GEMM op, or -1.  Op 14
+// with a fused add (params[15] != 0) carries the add operand at src[3].
+int ws_index(const int32_t *p) {
+    switch (p[13]) {
         case PPDL_OP_CONV:
-        case PPDL_OP_CONV1X1_BA:
         case PPDL_OP_CONV_IM2COL: return 3;
+        case PPDL_OP_CONV1X1_BA: return p[15] ? 4 : 3;
         case PPDL_OP_WG4_MADD: return 2;
         default: return -1;
     }
@@ -67,8 +68,8 @@ bool ws_valid(const ppdl_tview *t) {
     return t->ne[0] >= 1 && aligned16(t->data);
 }
 
-GemmWorkspace ws_of(int op, const ppdl_tview *src, int nsrc) {
-    const int i = ws_index(op);
+GemmWorkspace ws_of(const int32_t *p, const ppdl_tview *src, int nsrc) {
+    const int i = ws_index(p);
     if (i < 0 || nsrc <= i) return GemmWorkspace{nullptr, 0};
     return GemmWorkspace{src[i].data, nelem(&src[i]) * 4};
 }
@@ -87,13 +88,14 @@ int check_conv1x1(const int32_t *p, const ppdl_tview *dst, const ppdl_tview *src
     if (W * H > kMaxI32 || IC > kMaxI32 || OC > kMaxI32) return PPDL_EINVAL;
     if (fused) {
         if (!contig_f32(&src[2]) || nelem(&src[2]) != OC) return PPDL_EINVAL;
-        if (p[14] < 0 || p[14] > 2) return PPDL_EINVAL;
+        if (p[14] < 0 || p[14] > 2 || p[15] < 0 || p[15] > 2) return PPDL_EINVAL;
+        if (p[15] && (nsrc < 4 || !contig_f32(&src[3]) || !shape_is(&src[3], W, H, OC, 1))) return PPDL_EINVAL;
     }
     return PPDL_OK;
 }
 
 int check_op(const int32_t *p, const ppdl_tview *dst, const ppdl_tview *src, int nsrc) {
-    const int wi = ws_index(p[13]);
+    const int wi = ws_index(p);
     if (wi >= 0 && nsrc > wi && !ws_valid(&src[wi])) return PPDL_EINVAL;
     switch (p[13]) {
         case PPDL_OP_CONV: {
@@ -154,11 +156,11 @@ int check_op(const int32_t *p, const ppdl_tview *dst, const ppdl_tview *src, int
             const ppdl_tview *x = &src[0], *w = &src[1], *b = &src[2];
             if (!contig_f32(dst) || !contig_f32(x) || !contig_f32(w) || !contig_f32(b)) return PPDL_EINVAL;
             const int K = p[14] & 0xFF, S = (p[14] >> 8) & 0xFF, P = (p[14] >> 16) & 0xFF;
-            const int act = (p[14] >> 24) & 0xFF;
-            if (K < 1 || S < 1 || act > 2) return PPDL_EINVAL;
+            const int act = (p[14] >> 24) & 0xFF, PE = p[15];
+            if (K < 1 || S < 1 || act > 2 || PE < 0 || PE > 255) return PPDL_EINVAL;
             const int64_t IW = x->ne[0], IH = x->ne[1], IC = x->ne[2], OC = dst->ne[2];
-            if (IW + 2 * P < K || IH + 2 * P < K) return PPDL_EINVAL;
-            const int64_t OW = (IW + 2 * P - K) / S + 1, OH = (IH + 2 * P - K) / S + 1;
+            if (IW + 2 * P + PE < K || IH + 2 * P + PE < K) return PPDL_EINVAL;
+            const int64_t OW = (IW + 2 * P + PE - K) / S + 1, OH = (IH + 2 * P + PE - K) / S + 1;
             if (x->ne[3] != 1 || !shape_is(dst, OW, OH, OC, 1) || !shape_is(w, OC, IC, (int64_t)K * K, 1) ||
                 nelem(b) != OC)
                 return PPDL_EINVAL;
@@ -218,6 +220,10 @@ bool gemm_args_of(const int32_t *p, const ppdl_tview *dst, const ppdl_tview *src
             g->K = (int)x->ne[2];
             g->batch = 1;
             g->act = fused ? p[14] : 0;
+            if (fused && p[15]) {
+                g->add_mode = p[15];
+                g->add = (const float *)src[3].data;
+            }
             return true;
         }
         case PPDL_OP_WG4_MADD: {
@@ -273,7 +279,7 @@ extern "C" PPDL_HIP_API int64_t ppdl_hip_workspace_bytes(const int32_t op_params
     if (!op_params || (uint32_t)op_params[12] != (uint32_t)PPDL_MAGIC || !dst || nsrc < 0 ||
         (nsrc > 0 && !src))
         return -1;
-    const int wi = ws_index(op_params[13]);
+    const int wi = ws_index(op_params);
     const int n = (wi >= 0 && nsrc > wi) ? wi : nsrc;  // ignore a workspace already attached
     if (check_op(op_params, dst, src, n) != PPDL_OK) return -1;
     GemmArgs g;
@@ -310,7 +316,7 @@ extern "C" PPDL_HIP_API int ppdl_hip_run(const int32_t op_params[16], const ppdl
     GemmArgs g;
     bool im2col;
     if (gemm_args_of(p, dst, src, &g, &im2col)) {
-        const GemmWorkspace ws = ws_of(p[13], src, nsrc);
+        const GemmWorkspace ws = ws_of(p, src, nsrc);
         return status_of(im2col ? gemm_im2col(g, ws, s) : gemm_dense(g, ws, s));
     }
 
