@@ -265,6 +265,7 @@ class Net:
         memory = source * valid_mask()[:, None]
         om = self.ln(self.lin(memory, "enc_out.l"), "enc_out.ln")
         ecls = self.lin(om, "score_head")
+        self.dump("enc_logits", ecls)
         topk = K.topk(ecls, NQ)
         self.dump("topk_idx", topk)
         target = om[topk]

@@ -18,12 +18,13 @@ from conftest import normwise
 
 pytestmark = pytest.mark.gpu
 
-# Normwise tolerances (max|gpu - cpu| / max|cpu|).  Each conv GEMM is within
-# 2e-5 of the CPU restatement on its own; through ~150 sequential layers the
-# differences (summation order, Winograd F(4,3) vs im2col) compound, so the
-# deep intermediates get a looser gate than a single op.
-TOL_FEATURE = 2e-4
-TOL_OUTPUT = 5e-4
+# Normwise tolerances (max|gpu - cpu| / max|cpu|).  Each op is within 2e-5 of
+# the CPU restatement on its own; through ~150 sequential layers the
+# differences (summation order, Winograd F(4,3) vs im2col) could compound, so
+# the network-level gate is looser than the per-op one.  Measured on MI355X:
+# at most 7.4e-6 (enc_masks), most tensors 1e-6 .. 4e-6.
+TOL_FEATURE = 5e-5
+TOL_OUTPUT = 5e-5
 
 
 def say(*a):
@@ -74,11 +75,39 @@ def gpu(model, image, tmp_path_factory):
     ctx.close()
 
 
+# Tensors whose rows are the 300 decoder queries (in top-300 order).
+QUERY_ROWS = {"target", "enc_masks", "init_ref_unact", "hidden0", "hidden1", "hidden2", "hidden3", "hidden4",
+              "hidden5", "logits", "boxes", "masks", "init_ref"}
+
+
+def query_perm(gpu, cpu):
+    """p with gpu_topk[p] == cpu_topk: the GPU query order mapped onto the
+    CPU's.  The decoder treats every query alike (self-attention and the
+    heads are permutation-equivariant), so two tokens whose encoder scores
+    tie to rounding may swap places without changing any detection."""
+    g, c = gpu[1]["topk"], cpu[0]["topk"]
+    pos = {int(t): i for i, t in enumerate(g)}
+    return np.array([pos[int(t)] for t in c])
+
+
+def aligned(name, got, gpu, cpu):
+    p = query_perm(gpu, cpu)
+    if name == "order":
+        return got[p][:, p]
+    return got[p] if name in QUERY_ROWS else got
+
+
 def test_topk_selection_identical(gpu, cpu):
     _, raw, _, _, _ = gpu
     out = cpu[0]
+    # the same 300 tokens ...
     assert np.array_equal(np.sort(raw["topk"]), np.sort(out["topk"]))
-    assert np.array_equal(raw["topk"], out["topk"])
+    # ... in the same order up to swaps of tokens whose scores tie to rounding
+    score = cpu[1]["enc_logits"].max(1)
+    diff = np.where(raw["topk"] != out["topk"])[0]
+    gap = np.abs(score[raw["topk"][diff]] - score[out["topk"][diff]])
+    say("top-300 positions that differ:", diff.tolist(), "score gaps", gap.tolist())
+    assert np.all(gap <= 1e-4 * np.abs(score).max())
 
 
 @pytest.mark.parametrize("name", ["stem1", "stem", "st0", "st1", "st2", "st3", "aifi", "f8", "n16", "n32",
@@ -87,7 +116,7 @@ def test_topk_selection_identical(gpu, cpu):
 def test_intermediate_matches_cpu(gpu, cpu, name):
     dumps = gpu[2]
     ref = cpu[1][name]
-    got = dumps[name]
+    got = aligned(name, dumps[name], gpu, cpu)
     assert got.shape == ref.shape, (name, got.shape, ref.shape)
     assert np.isfinite(got).all()
     err = normwise(got, ref)
@@ -97,7 +126,7 @@ def test_intermediate_matches_cpu(gpu, cpu, name):
 
 @pytest.mark.parametrize("name", ["logits", "boxes", "order", "masks", "init_ref"])
 def test_raw_output_matches_cpu(gpu, cpu, name):
-    got = gpu[1][name]
+    got = aligned(name, gpu[1][name], gpu, cpu)
     ref = cpu[0][name]
     assert got.shape == ref.shape
     err = normwise(got, ref)
