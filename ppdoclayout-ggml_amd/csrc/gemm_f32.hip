@@ -140,7 +140,9 @@ __global__ __launch_bounds__(kThreads) void k_gemm(GemmArgs g, SplitArgs sp, int
         iy0 = oy * g.S - g.P;
         ix0 = ox * g.S - g.P;
     }
-    const int64_t plane = (int64_t)g.IH * g.IW;
+    // operand extents per batch plane fit in int32 (checked on the host)
+    const int plane = g.IH * g.IW;
+    const int lda = (int)g.lda, ldb = (int)g.ldb;
 
     f32x16 acc[TM][TN];
 #pragma unroll
@@ -153,22 +155,48 @@ __global__ __launch_bounds__(kThreads) void k_gemm(GemmArgs g, SplitArgs sp, int
     const int wm0 = (wave % WGM) * WM, wn0 = (wave / WGM) * WN;
     const int l32 = lane & 31, lk = (lane >> 5) * KH;
 
+    // One k tile = KH MFMA steps, taken in pairs: a pair's A and B fragments
+    // are two adjacent k rows (one ds_read2 per 32-wide strip).  Fragments
+    // are read two pairs ahead of the MFMAs that use them, and the schedule
+    // is pinned (sched_group_barrier) so each pair's reads issue behind the
+    // previous pair's MFMAs: LDS latency hides under the matrix pipe even
+    // with a single wave per SIMD.
+    constexpr int NP = KH / 2;
     auto compute = [&](int buf) {
-        float a[KH][TM], b[KH][TN];
+        float2 fa[NP][TM], fb[NP][TN];
+        auto rd = [&](int p) {
 #pragma unroll
-        for (int kk = 0; kk < KH; kk++) {
+            for (int i = 0; i < TM; i++) {
+                fa[p][i].x = As[buf][lk + 2 * p][wm0 + i * 32 + l32];
+                fa[p][i].y = As[buf][lk + 2 * p + 1][wm0 + i * 32 + l32];
+            }
 #pragma unroll
-            for (int i = 0; i < TM; i++) a[kk][i] = As[buf][lk + kk][wm0 + i * 32 + l32];
+            for (int j = 0; j < TN; j++) {
+                fb[p][j].x = Bs[buf][lk + 2 * p][wn0 + j * 32 + l32];
+                fb[p][j].y = Bs[buf][lk + 2 * p + 1][wn0 + j * 32 + l32];
+            }
+        };
+        rd(0);
+        rd(1);
+        __builtin_amdgcn_sched_group_barrier(0x100, 2 * (TM + TN), 0);
 #pragma unroll
-            for (int j = 0; j < TN; j++) b[kk][j] = Bs[buf][lk + kk][wn0 + j * 32 + l32];
-        }
-#pragma unroll
-        for (int kk = 0; kk < KH; kk++)
+        for (int p = 0; p < NP; p++) {
 #pragma unroll
             for (int i = 0; i < TM; i++)
 #pragma unroll
                 for (int j = 0; j < TN; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[kk][i], b[kk][j], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[p][i].x, fb[p][j].x, acc[i][j], 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int j = 0; j < TN; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[p][i].y, fb[p][j].y, acc[i][j], 0, 0, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 2 * TM * TN, 0);
+            if (p + 2 < NP) {
+                rd(p + 2);
+                __builtin_amdgcn_sched_group_barrier(0x100, TM + TN, 0);
+            }
+        }
     };
 
     // The loads only issue (clamped, always-valid addresses); every mask is
@@ -185,7 +213,7 @@ __global__ __launch_bounds__(kThreads) void k_gemm(GemmArgs g, SplitArgs sp, int
 #pragma unroll
                 for (int e = 0; e < EA; e++) {
                     const int k = min(k0 + ak + e * RA, K - 1);
-                    const float *row = A + (int64_t)k * g.lda;
+                    const float *row = A + (uint32_t)(k * lda);
                     if (!EDGE) {
                         r.a[e] = ld4(row + gm);
                     } else {
@@ -202,14 +230,14 @@ __global__ __launch_bounds__(kThreads) void k_gemm(GemmArgs g, SplitArgs sp, int
 #pragma unroll
                 for (int e = 0; e < EA; e++) {
                     const int m = min(m0 + amr + e * RA1, M - 1);
-                    r.a[e] = ld4(A + (int64_t)m * g.lda + k);
+                    r.a[e] = ld4(A + (uint32_t)(m * lda + k));
                 }
             }
             if (BMODE == 0) {
 #pragma unroll
                 for (int e = 0; e < EB4; e++) {
                     const int k = min(k0 + bk4 + e * RB4, K - 1);
-                    const float *row = B + (int64_t)k * g.ldb;
+                    const float *row = B + (uint32_t)(k * ldb);
                     if (!EDGE) {
                         r.b4[e] = ld4(row + gn4);
                     } else {
@@ -232,7 +260,7 @@ __global__ __launch_bounds__(kThreads) void k_gemm(GemmArgs g, SplitArgs sp, int
                 for (int e = 0; e < EB1; e++) {
                     const int iy = iy0 + kh, ix = ix0 + kw;
                     const bool ok = bn_ok && k < K && iy >= 0 && iy < g.IH && ix >= 0 && ix < g.IW;
-                    r.b1[e] = B[ok ? ic * plane + (int64_t)iy * g.IW + ix : 0];
+                    r.b1[e] = B[ok ? (uint32_t)(ic * plane + iy * g.IW + ix) : 0u];
                     okm |= (ok ? 1u : 0u) << e;
                     k += RB1;
                     ic += RB1;
@@ -289,10 +317,13 @@ __global__ __launch_bounds__(kThreads) void k_gemm(GemmArgs g, SplitArgs sp, int
             }
         };
 
-        // two-deep pipeline: r0/r1 alternate as the staging registers of even
-        // / odd k tiles, LDS buffer 0/1 likewise.  Prefetches past the last
-        // tile reload the last tile (never stored): keeping every load
-        // unconditional keeps the in-flight count static.
+        // Two-deep pipeline: r0/r1 alternate as the staging registers of even
+        // / odd k tiles, LDS buffer 0/1 likewise.  A trip takes two tiles and
+        // has no exit in the middle (an exit there leaves a path on which the
+        // prefetch is still in flight at the loop head, and every trip then
+        // drains it); an odd last tile is computed after the loop.  Loads and
+        // stores past the last tile repeat the last tile (clamped), so every
+        // trip issues the same instructions; those stages are never read.
         if (nk <= 0) return;  // an empty split range contributes zeros
         const int klast = kt1 - 1;
         St r0, r1;
@@ -300,17 +331,24 @@ __global__ __launch_bounds__(kThreads) void k_gemm(GemmArgs g, SplitArgs sp, int
         store(r0, 0, kt0);
         load(r1, min(kt0 + 1, klast));
         __syncthreads();
-        for (int it = 0; it < nk; it += 2) {
+        int it = 0;
+        for (; it + 1 < nk; it += 2) {
             load(r0, min(kt0 + it + 2, klast));
+            // keep the prefetch ahead of the MFMAs (sunk below them, its
+            // destination registers get recycled as fragment registers)
+            __builtin_amdgcn_sched_barrier(0);
             compute(0);
-            if (it + 1 < nk) store(r1, 1, kt0 + it + 1);
+            __builtin_amdgcn_sched_barrier(0);
+            store(r1, 1, kt0 + it + 1);
             __syncthreads();
-            if (it + 1 >= nk) break;
             load(r1, min(kt0 + it + 3, klast));
+            __builtin_amdgcn_sched_barrier(0);
             compute(1);
-            if (it + 2 < nk) store(r0, 0, kt0 + it + 2);
+            __builtin_amdgcn_sched_barrier(0);
+            store(r0, 0, min(kt0 + it + 2, klast));
             __syncthreads();
         }
+        if (it < nk) compute(0);
     };
     if (m0 + BM > M || n0 + BN > N)
         body(std::true_type{});
@@ -488,6 +526,10 @@ hipError_t launch(const GemmArgs &g, int S, const GemmWorkspace &ws, hipStream_t
     const int64_t tiles = (int64_t)tiles_m * tiles_n * g.batch;
     const int64_t total = tiles * S;
     if (total <= 0 || total > 0x7fffffff) return hipErrorInvalidValue;
+    // the kernel addresses A and B within one batch plane with 32-bit offsets
+    const int64_t a_ext = AMODE == 0 ? (int64_t)g.K * g.lda : (int64_t)g.M * g.lda;
+    const int64_t b_ext = BMODE == 0 ? (int64_t)g.K * g.ldb : (int64_t)g.IC * g.IH * g.IW;
+    if (a_ext + BM > 0x7fffffff || b_ext + BN > 0x7fffffff) return hipErrorInvalidValue;
     SplitArgs sp{1, 0, nullptr};
     if (S > 1) {
         const int nk = (g.K + kBK - 1) / kBK;
