@@ -97,7 +97,9 @@ PPDL_HIP_API int ppdl_hip_supports(const int32_t op_params[16], const ppdl_tview
  *  12 WG4_MADD  src: dt ne(T,IC,36), wg4 ne(OC,IC,36); dst yt ne(T,OC,36):
  *               yt[p][oc][t] = sum_ic dt[p][ic][t] * wg4[p][ic][oc].
  *  1  MASKBOX   src: mask logits ne(40000,NQ); dst ne(4,NQ).
- *  13 TOPK      src: class logits ne(NC,NTOK), NTOK <= 13312; dst I32 ne(NQ).
+ *  13 TOPK      src: class logits ne(NC,NTOK), NTOK <= 13312; dst I32 ne(NQ):
+ *               token indices by max-class logit, descending, ties to the
+ *               lower index.
  *  14 CONV1X1_BA as op 3 plus bias/act: params[14] = act; params[15] = add
  *               mode: 0 none, 1 dst = act(conv + bias + src[3]), 2 dst =
  *               act(conv + bias) + src[3]; src[3] has dst's shape.
@@ -117,12 +119,17 @@ PPDL_HIP_API int ppdl_hip_supports(const int32_t op_params[16], const ppdl_tview
  * with fewer or no K splits: results differ only by fp32 summation order, and
  * a given plan always sums in the same order.  Ops sharing one workspace must
  * not run concurrently.
+ *
+ * Op 13 takes the same kind of optional workspace as src[1] (8 bytes per
+ * token): with it the per-token keys are computed by a grid-wide kernel
+ * before the one-block selection; without it the selection block computes
+ * them itself (slower, same result).
  */
 PPDL_HIP_API int ppdl_hip_run(const int32_t op_params[16], const ppdl_tview *dst,
                               const ppdl_tview *src, int nsrc, void *stream);
 
-/* Workspace bytes the node's GEMM plan would use (0 = needs none), or -1 if
- * the node is invalid.  Host-only; no counterpart in the reference, whose
+/* Workspace bytes the node would use (GEMM ops: its split-K plan, 0 = needs
+ * none; op 13: 8 per token), or -1 if the node is invalid.  Host-only; no counterpart in the reference, whose
  * GEMMs run in cuBLAS with the backend's own workspace. */
 PPDL_HIP_API int64_t ppdl_hip_workspace_bytes(const int32_t op_params[16], const ppdl_tview *dst,
                                               const ppdl_tview *src, int nsrc);

@@ -163,8 +163,10 @@ __global__ __launch_bounds__(256) void k_mask_box(const float *__restrict__ ml,
 // Each token gets a unique 64-bit key: order-preserving float bits (with -0
 // folded into +0, since the CPU comparison treats them as equal) in the high
 // word and the bit-inverted index in the low word, so "larger key" is exactly
-// the CPU order.  A radix select over the 8 key bytes finds the NQ-th largest
-// key; the keys at or above it are gathered and bitonic-sorted in LDS.
+// the CPU order.  A radix select over the key bytes finds a threshold with
+// exactly NQ keys at or above it; those are gathered in LDS and each is placed
+// by counting the gathered keys above it.  With a workspace, the keys are
+// first computed by a grid-wide kernel.
 constexpr int kTopkThreads = 1024;
 constexpr int kTopkPer = 13;  // 13 * 1024 = 13312 >= 13125
 constexpr int kTopkSort = 512;
@@ -176,12 +178,29 @@ __device__ __forceinline__ uint64_t topk_key(float m, int idx) {
     return ((uint64_t)u << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)idx);
 }
 
+__device__ __forceinline__ float row_max(const float *p, int nc) {
+    float m = p[0];
+    for (int c = 1; c < nc; c++) m = (m < p[c]) ? p[c] : m;
+    return m;
+}
+
+// One key per token, over the whole grid (the selection kernel then reads
+// 8 bytes per token instead of a row of logits).
+__global__ __launch_bounds__(256) void k_topk_keys(const float *__restrict__ lg, uint64_t *__restrict__ keys,
+                                                   int ntok, int nc) {
+    const int t = blockIdx.x * 256 + threadIdx.x;
+    if (t < ntok) keys[t] = topk_key(row_max(lg + (int64_t)t * nc, nc), t);
+}
+
+// keys == nullptr: the block computes the keys from the logits itself
 __global__ __launch_bounds__(kTopkThreads) void k_topk(const float *__restrict__ lg,
+                                                       const uint64_t *__restrict__ keys,
                                                        int32_t *__restrict__ out, int ntok, int nc,
                                                        int nq) {
     __shared__ uint32_t hist[256];
+    __shared__ uint32_t whist[kTopkThreads / 64][256];
     __shared__ uint64_t sel[kTopkSort];
-    __shared__ int s_digit, s_rank, s_cnt;
+    __shared__ int s_digit, s_rank, s_cnt, s_done;
     const int tid = threadIdx.x;
 
     uint64_t key[kTopkPer];
@@ -189,24 +208,35 @@ __global__ __launch_bounds__(kTopkThreads) void k_topk(const float *__restrict__
     for (int j = 0; j < kTopkPer; j++) {
         const int t = tid + j * kTopkThreads;
         key[j] = 0;  // below every real key (real keys have a nonzero low word or high word)
-        if (t < ntok) {
-            const float *p = lg + (int64_t)t * nc;
-            float m = p[0];
-            for (int c = 1; c < nc; c++) m = (m < p[c]) ? p[c] : m;
-            key[j] = topk_key(m, t);
-        }
+        if (t < ntok) key[j] = keys ? keys[t] : topk_key(row_max(lg + (int64_t)t * nc, nc), t);
     }
 
-    // radix select: after the loop, `prefix` is the NQ-th largest key
+    // Radix select, most significant byte first.  Each pass histograms the
+    // byte of the keys that still match the selected prefix; each wave counts
+    // into a histogram of its own (nearly all keys share their top bytes, and
+    // one shared histogram serialises those atomics over the whole block).
+    // The pass that lands on a bin holding exactly the remaining rank ends
+    // the search: every key of that bin is selected, so the threshold is the
+    // prefix with its lower bytes zero.
+    constexpr int kWaves = kTopkThreads / 64;
+    uint32_t *wh = &whist[0][0];
+    const int wave = tid >> 6;
     uint64_t prefix = 0, mask = 0;
     int rank = nq;  // 1-based rank still to find within the current prefix
     for (int byte = 7; byte >= 0; byte--) {
-        for (int i = tid; i < 256; i += kTopkThreads) hist[i] = 0;
+        for (int i = tid; i < kWaves * 256; i += kTopkThreads) wh[i] = 0;
         __syncthreads();
         const int sh = byte * 8;
 #pragma unroll
         for (int j = 0; j < kTopkPer; j++)
-            if ((key[j] & mask) == prefix && key[j] != 0) atomicAdd(&hist[(key[j] >> sh) & 0xFF], 1u);
+            if ((key[j] & mask) == prefix && key[j] != 0) atomicAdd(&whist[wave][(key[j] >> sh) & 0xFF], 1u);
+        __syncthreads();
+        if (tid < 256) {
+            uint32_t c = 0;
+#pragma unroll
+            for (int w = 0; w < kWaves; w++) c += whist[w][tid];
+            hist[tid] = c;
+        }
         __syncthreads();
         if (tid < 64) {
             // wave 0 scans the 256 bins from the top: 4 bins per lane
@@ -228,6 +258,7 @@ __global__ __launch_bounds__(kTopkThreads) void k_topk(const float *__restrict__
                 if (run < (uint32_t)rank && run + c4[b] >= (uint32_t)rank) {
                     s_digit = 255 - (tid * 4 + b);
                     s_rank = rank - (int)run;
+                    s_done = c4[b] == (uint32_t)(rank - (int)run);
                 }
                 run += c4[b];
             }
@@ -236,11 +267,12 @@ __global__ __launch_bounds__(kTopkThreads) void k_topk(const float *__restrict__
         prefix |= (uint64_t)s_digit << sh;
         mask |= (uint64_t)0xFF << sh;
         rank = s_rank;
+        const int done = s_done;
         __syncthreads();
+        if (done) break;
     }
 
     // gather keys >= threshold (exactly nq of them: keys are unique)
-    for (int i = tid; i < kTopkSort; i += kTopkThreads) sel[i] = 0;
     if (tid == 0) s_cnt = 0;
     __syncthreads();
 #pragma unroll
@@ -252,25 +284,14 @@ __global__ __launch_bounds__(kTopkThreads) void k_topk(const float *__restrict__
     }
     __syncthreads();
 
-    // bitonic sort, descending
-    for (int k = 2; k <= kTopkSort; k <<= 1) {
-        for (int j = k >> 1; j > 0; j >>= 1) {
-            for (int i = tid; i < kTopkSort; i += kTopkThreads) {
-                const int ixj = i ^ j;
-                if (ixj > i) {
-                    const uint64_t a = sel[i], b = sel[ixj];
-                    const bool desc = (i & k) == 0;
-                    if (desc ? (a < b) : (a > b)) {
-                        sel[i] = b;
-                        sel[ixj] = a;
-                    }
-                }
-            }
-            __syncthreads();
-        }
+    // each selected key's position is the number of selected keys above it
+    const int cnt = min(s_cnt, kTopkSort);
+    for (int i = tid; i < cnt; i += kTopkThreads) {
+        const uint64_t ki = sel[i];
+        int r = 0;
+        for (int j = 0; j < cnt; j++) r += sel[j] > ki ? 1 : 0;
+        if (r < nq) out[r] = (int32_t)(0xFFFFFFFFu - (uint32_t)(ki & 0xFFFFFFFFu));
     }
-    for (int r = tid; r < nq; r += kTopkThreads)
-        out[r] = (int32_t)(0xFFFFFFFFu - (uint32_t)(sel[r] & 0xFFFFFFFFu));
 }
 
 }  // namespace
@@ -286,8 +307,16 @@ hipError_t mask_box(const float *ml, float *out, int nq, hipStream_t s) {
     return hipGetLastError();
 }
 
-hipError_t topk(const float *logits, int32_t *out, int ntok, int nc, int nq, hipStream_t s) {
-    hipLaunchKernelGGL(k_topk, dim3(1), dim3(kTopkThreads), 0, s, logits, out, ntok, nc, nq);
+hipError_t topk(const float *logits, int32_t *out, int ntok, int nc, int nq, void *ws, int64_t ws_bytes,
+                hipStream_t s) {
+    uint64_t *keys = nullptr;
+    if (ws && ws_bytes >= (int64_t)ntok * 8) {
+        keys = (uint64_t *)ws;
+        hipLaunchKernelGGL(k_topk_keys, dim3((ntok + 255) / 256), dim3(256), 0, s, logits, keys, ntok, nc);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL(k_topk, dim3(1), dim3(kTopkThreads), 0, s, logits, keys, out, ntok, nc, nq);
     return hipGetLastError();
 }
 

@@ -470,6 +470,119 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(const float *__restrict__
     }
 }
 
+// ---------------------------------------------------------------------------
+// Small-GEMM path: for shapes whose 64x64 tiling leaves most of the chip idle
+// (the decoder's 300-token linears, the backbone's last stages).  A block owns
+// a 32x32 output tile and its 4 waves split K: wave w contracts k chunks
+// w, w+4, ... of 64.  Fragments come straight from global memory into
+// registers in MFMA operand order (no LDS staging), with the next chunk's
+// loads issued before the current chunk's MFMAs, so a wave pays about one
+// memory latency per two chunks instead of one per k tile.  The 4 partial
+// tiles are summed through LDS in fixed wave order (deterministic) and the
+// usual epilogue applies.
+//
+// Operand order per chunk (kb = chunk start): step s = 4c + j (c < 8, j < 4)
+// pairs k = kb + 8c + j (lanes 0-31) with k = kb + 8c + 4 + j (lanes 32-63);
+// A and B use the same pairing, so the sum covers every k once.  A row-major
+// (AMODE 1) is then one float4 per lane per c.
+template <int AMODE>
+__global__ __launch_bounds__(kThreads) void k_gemm_small(GemmArgs g, int tiles_m, int tiles_mn) {
+    constexpr int KC = 64, NS = KC / 2;
+    __shared__ float red[4][32][33];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int l32 = lane & 31, h = lane >> 5;
+    const int logical = xcd_remap(blockIdx.x, gridDim.x);
+    const int bz = logical / tiles_mn;
+    const int t = logical - bz * tiles_mn;
+    const int m0 = (t % tiles_m) * 32, n0 = (t / tiles_m) * 32;
+    const int M = g.M, N = g.N, K = g.K;
+    const int lda = (int)g.lda, ldb = (int)g.ldb;
+    const float *__restrict__ A = g.A + (int64_t)bz * g.sA;
+    const float *__restrict__ B = g.B + (int64_t)bz * g.sB;
+    const int mc = min(m0 + l32, M - 1), nc = min(n0 + l32, N - 1);
+    const int nchunk = (K + KC - 1) / KC;
+
+    auto load = [&](float (&a)[NS], float (&b)[NS], int ch) {
+        const int kb = ch * KC;
+#pragma unroll
+        for (int c = 0; c < 8; c++) {
+            const int k4 = kb + 8 * c + 4 * h;  // this lane's 4 consecutive k
+            if (AMODE == 1) {
+                // K % 4 == 0: the 4 k are all inside or all outside
+                const float4 v = ld4(A + (uint32_t)(mc * lda + min(k4, K - 4)));
+                const bool in = k4 < K;
+                a[4 * c + 0] = in ? v.x : 0.0f;
+                a[4 * c + 1] = in ? v.y : 0.0f;
+                a[4 * c + 2] = in ? v.z : 0.0f;
+                a[4 * c + 3] = in ? v.w : 0.0f;
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const int k = k4 + j;
+                    const float v = A[(uint32_t)(min(k, K - 1) * lda + mc)];
+                    a[4 * c + j] = k < K ? v : 0.0f;
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int k = k4 + j;
+                const float v = B[(uint32_t)(min(k, K - 1) * ldb + nc)];
+                b[4 * c + j] = k < K ? v : 0.0f;
+            }
+        }
+    };
+
+    f32x16 acc;
+#pragma unroll
+    for (int r = 0; r < 16; r++) acc[r] = 0.0f;
+    float a0[NS], b0[NS], a1[NS], b1[NS];
+    auto mma = [&](const float (&a)[NS], const float (&b)[NS]) {
+#pragma unroll
+        for (int st = 0; st < NS; st++) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[st], b[st], acc, 0, 0, 0);
+    };
+    // chunks of this wave: wave, wave + 4, ...; two register stages
+    int ch = wave;
+    if (ch < nchunk) load(a0, b0, ch);
+    while (ch < nchunk) {
+        if (ch + 4 < nchunk) load(a1, b1, ch + 4);
+        __builtin_amdgcn_sched_barrier(0);
+        mma(a0, b0);
+        __builtin_amdgcn_sched_barrier(0);
+        ch += 4;
+        if (ch >= nchunk) break;
+        if (ch + 4 < nchunk) load(a0, b0, ch + 4);
+        __builtin_amdgcn_sched_barrier(0);
+        mma(a1, b1);
+        __builtin_amdgcn_sched_barrier(0);
+        ch += 4;
+    }
+
+    // accumulator: lane owns column l32, rows 8(r/4) + 4h + r%4
+#pragma unroll
+    for (int r = 0; r < 16; r++) red[wave][8 * (r >> 2) + 4 * h + (r & 3)][l32] = acc[r];
+    __syncthreads();
+
+    const float *__restrict__ bias = g.bias;
+    float *__restrict__ C = g.C + (int64_t)bz * g.sC;
+    const float *__restrict__ Ad = g.add ? g.add + (int64_t)bz * g.sC : nullptr;
+    // 256 threads x 4 outputs; consecutive threads along the contiguous axis of C
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int fast = tid & 31, slow = (tid >> 5) + 8 * i;
+        const int mm = g.c_trans ? fast : slow, nn = g.c_trans ? slow : fast;
+        const int m = m0 + mm, n = n0 + nn;
+        if (m < M && n < N) {
+            float v = ((red[0][mm][nn] + red[1][mm][nn]) + red[2][mm][nn]) + red[3][mm][nn];
+            const int64_t idx = g.c_trans ? (int64_t)n * g.ldc + m : (int64_t)m * g.ldc + n;
+            if (bias) v += bias[g.bias_n ? n : m];
+            if (g.add_mode == 1) v += Ad[idx];
+            v = act_f(v, g.act);
+            if (g.add_mode == 2) v += Ad[idx];
+            C[idx] = v;
+        }
+    }
+}
+
 struct TileCfg {
     int bm, bn, wgm;
 };
@@ -483,6 +596,7 @@ constexpr TileCfg kCfgs[] = {
     {32, 128, 1},   // 5: wave 32x32
 };
 constexpr int kNumCfg = sizeof(kCfgs) / sizeof(kCfgs[0]);
+constexpr int kCfgSmall = kNumCfg;  // the small-GEMM kernel (32x32 tiles, K split over waves)
 constexpr int kSplitChoices[] = {1, 2, 3, 4, 6, 8, 12, 16};
 
 int64_t tiles_of(int c, int M, int N, int batch) {
@@ -495,7 +609,14 @@ int64_t tiles_of(int c, int M, int N, int batch) {
 // won or tied nearly everywhere; 32-row blocks when M <= 32.  Splitting K
 // paid only when the output had too few tiles to occupy the chip: the best
 // S kept about 1000 blocks in flight with at least 6 k tiles per split.
-GemmPlan plan_auto(int M, int N, int K, int batch) {
+GemmPlan plan_auto(int M, int N, int K, int batch, bool im2col) {
+    // Few output tiles and a small operand footprint: the small-GEMM kernel
+    // (32x32 tiles, K split over the block's waves, no split-K pass).  Its
+    // L2 traffic grows with the tile count (each operand is re-read once per
+    // 32-wide strip of the other), hence the footprint bound.
+    const int64_t t64 = (int64_t)((M + 63) / 64) * ((N + 63) / 64) * batch;
+    const int64_t reread = 4 * ((int64_t)M * K * ((N + 31) / 32) + (int64_t)K * N * ((M + 31) / 32)) * batch;
+    if (!im2col && t64 < 200 && reread <= ((int64_t)40 << 20)) return GemmPlan{kCfgSmall, 1};
     GemmPlan p{M <= 32 ? 5 : 3, 1};
     const int nk = (K + kBK - 1) / kBK;
     const int64_t tiles = tiles_of(p.cfg, M, N, batch);
@@ -514,7 +635,7 @@ int env_override(int *cfg, int *splits) {
     char *end = nullptr;
     const int oc = (int)strtol(e, &end, 10);
     const int os = (end && *end == ',') ? (int)strtol(end + 1, nullptr, 10) : 1;
-    if (oc < 0 || oc >= kNumCfg) return 0;
+    if (oc < 0 || oc > kCfgSmall) return 0;
     *cfg = oc;
     *splits = os < 1 ? 1 : os;
     return 1;
@@ -555,9 +676,26 @@ hipError_t launch(const GemmArgs &g, int S, const GemmWorkspace &ws, hipStream_t
     return hipGetLastError();
 }
 
+template <int AMODE>
+hipError_t launch_small(const GemmArgs &g, hipStream_t s) {
+    const int tiles_m = (g.M + 31) / 32, tiles_n = (g.N + 31) / 32;
+    const int64_t total = (int64_t)tiles_m * tiles_n * g.batch;
+    const int64_t a_ext = AMODE == 0 ? (int64_t)g.K * g.lda : (int64_t)g.M * g.lda;
+    if (total <= 0 || total > 0x7fffffff || a_ext > 0x7fffffff || (int64_t)g.K * g.ldb > 0x7fffffff)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_gemm_small<AMODE>, dim3((unsigned)total), dim3(kThreads), 0, s, g, tiles_m,
+                       tiles_m * tiles_n);
+    return hipGetLastError();
+}
+
 template <int BMODE>
 hipError_t dispatch(const GemmArgs &g, const GemmWorkspace &ws, hipStream_t s) {
-    const GemmPlan p = gemm_plan(g, ws.bytes);
+    const GemmPlan p = gemm_plan(g, ws.bytes, BMODE == 1);
+    if (BMODE == 0 && p.cfg == kCfgSmall) {
+        if (g.a_rowmajor && (g.K % 4 != 0 || g.lda % 4 != 0 || (((uintptr_t)g.A) & 15) != 0))
+            return hipErrorInvalidValue;
+        return g.a_rowmajor ? launch_small<1>(g, s) : launch_small<0>(g, s);
+    }
     if (g.a_rowmajor) {
         // row-major A (token-major activations) is built for the two block
         // shapes the planner uses
@@ -584,23 +722,24 @@ int64_t gemm_ws_bytes(int M, int N, int batch, int cfg, int splits) {
     return (int64_t)splits * batch * M * N * 4;
 }
 
-GemmPlan gemm_plan(const GemmArgs &g, int64_t ws_bytes) {
+GemmPlan gemm_plan(const GemmArgs &g, int64_t ws_bytes, bool im2col) {
     GemmPlan best;
     int oc, os;
     const int nk = (g.K + kBK - 1) / kBK;
     if (env_override(&oc, &os)) {
+        if (oc == kCfgSmall && im2col) oc = 3;  // the small kernel reads dense B only
         best.cfg = oc;
-        best.splits = os < nk ? os : nk;  // at most one split per k tile
+        best.splits = oc == kCfgSmall ? 1 : (os < nk ? os : nk);  // at most one split per k tile
     } else {
-        best = plan_auto(g.M, g.N, g.K, g.batch);
+        best = plan_auto(g.M, g.N, g.K, g.batch, im2col);
     }
     // never plan more splits than the workspace holds
     while (best.splits > 1 && gemm_ws_bytes(g.M, g.N, g.batch, best.cfg, best.splits) > ws_bytes) best.splits--;
     return best;
 }
 
-int64_t gemm_ws_bytes_for(const GemmArgs &g) {
-    const GemmPlan p = gemm_plan(g, INT64_MAX);
+int64_t gemm_ws_bytes_for(const GemmArgs &g, bool im2col) {
+    const GemmPlan p = gemm_plan(g, INT64_MAX, im2col);
     return gemm_ws_bytes(g.M, g.N, g.batch, p.cfg, p.splits);
 }
 

@@ -177,7 +177,7 @@ class Net {
         });
     }
     void gemm(const std::string &name, GemmArgs g) {
-        const int64_t wsb = gemm_ws_bytes_for(g);
+        const int64_t wsb = gemm_ws_bytes_for(g, false);
         ws_need_ = std::max(ws_need_, wsb);
         node(name, wsb > 0 ? 2 : 1, [this, g, wsb](hipStream_t s) {
             GemmWorkspace ws{wsb > 0 ? ws_ : nullptr, wsb > 0 ? ws_bytes_ : 0};

@@ -148,77 +148,129 @@ __global__ __launch_bounds__(256) void k_layernorm(const float *__restrict__ a, 
 // ---------------------------------------------------------------------------
 // Multi-head attention core (src/ppdoclayout.cpp:572-587): per head h,
 // out[t][h*32+c] = sum_s softmax_s(q_t . k_s / sqrt(32)) v[s][h*32+c].
-// q, k, v are token-major with row strides ldq/ldk/ldv.  A block owns one
-// head and 64 queries; 4 threads per query each cover a quarter of the keys
-// with an online softmax, then merge.  Keys/values stream through LDS in
-// chunks of 64.
-constexpr int kAttQ = 64, kAttKC = 64;
+// q, k, v are token-major with row strides ldq/ldk/ldv.
+//
+// On the FP32 matrix cores (v_mfma_f32_32x32x2_f32).  A block owns one head
+// and 32 queries; its 4 waves take interleaved 32-key chunks and keep an
+// online softmax each, merged at the end.  Per chunk a wave computes the
+// transposed scores S^T = K Q^T (32 keys x 32 queries), so each lane's
+// accumulator column is one query: the row max / sum over keys stay within a
+// lane pair, and the accumulator registers of S^T are directly the B operand
+// of O^T += V^T P^T (register r holds keys 8(r/4) + r%4 in lanes 0-31 and 4
+// more in lanes 32-63, which fixes the key each lane supplies on the A side).
+// K and V chunks pass through a per-wave LDS slice; no block barrier until
+// the merge.
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+constexpr int kAttQ = 32, kAttWaves = 4;
 
 __global__ __launch_bounds__(256) void k_attention(const float *__restrict__ q, int ldq,
                                                    const float *__restrict__ k, int ldk,
                                                    const float *__restrict__ v, int ldv, float *__restrict__ out,
                                                    int ldo, int T, float scale) {
-    __shared__ float Ks[kAttKC][kHD + 1];
-    __shared__ float Vs[kAttKC][kHD + 1];
-    __shared__ float red_m[kAttQ][4], red_l[kAttQ][4];
-    __shared__ float red_o[kAttQ][4][kHD + 1];
-    const int h = blockIdx.y;
-    const int qi = threadIdx.x >> 2, part = threadIdx.x & 3;
-    const int t = blockIdx.x * kAttQ + qi;
-    const bool live = t < T;
-    float qv[kHD], acc[kHD];
+    __shared__ float Ks[kAttWaves][32][kHD + 1];
+    __shared__ float Vs[kAttWaves][32][kHD + 1];
+    __shared__ float mw[kAttWaves][kAttQ], lw[kAttWaves][kAttQ];
+    __shared__ float ow[kAttWaves][kHD][kAttQ + 1];
+    const int h = blockIdx.y, q0 = blockIdx.x * kAttQ;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int l32 = lane & 31, hi = lane >> 5;
+
+    // B operand of S^T: Q^T[d][q], lane supplies d = 2*st + hi of query l32
+    float qf[kHD / 2];
+    {
+        const int t = q0 + l32;
+        const float *qr = q + (int64_t)min(t, T - 1) * ldq + h * kHD + hi;
 #pragma unroll
-    for (int c = 0; c < kHD; c++) {
-        qv[c] = live ? q[(int64_t)t * ldq + h * kHD + c] : 0.0f;
-        acc[c] = 0.0f;
+        for (int st = 0; st < kHD / 2; st++) qf[st] = t < T ? qr[2 * st] : 0.0f;
     }
-    float mx = -INFINITY, l = 0.0f;
-    for (int s0 = 0; s0 < T; s0 += kAttKC) {
-        __syncthreads();
-        for (int i = threadIdx.x; i < kAttKC * kHD; i += 256) {
-            const int r = i / kHD, c = i - r * kHD;
-            const int s = s0 + r;
-            Ks[r][c] = s < T ? k[(int64_t)s * ldk + h * kHD + c] : 0.0f;
-            Vs[r][c] = s < T ? v[(int64_t)s * ldv + h * kHD + c] : 0.0f;
-        }
-        __syncthreads();
-        const int n = min(kAttKC, T - s0);
-        for (int r = part; r < n; r += 4) {
-            float d = 0.0f;
+    f32x16_t o;
 #pragma unroll
-            for (int c = 0; c < kHD; c++) d = fmaf(qv[c], Ks[r][c], d);
-            d *= scale;
-            if (d > mx) {
-                const float corr = expf(mx - d);
-                l *= corr;
+    for (int r = 0; r < 16; r++) o[r] = 0.0f;
+    float m = -INFINITY, lsum = 0.0f;
+
+    for (int c = wave; c * 32 < T; c += kAttWaves) {
+        const int key0 = c * 32;
+        {
+            // lane: key row lane/2, 16 consecutive channels (lane%2)*16
+            const int row = lane >> 1, c0 = (lane & 1) * 16, s_ = key0 + row;
+            const bool in = s_ < T;
+            const float4 *kr = reinterpret_cast<const float4 *>(k + (int64_t)min(s_, T - 1) * ldk + h * kHD + c0);
+            const float4 *vr = reinterpret_cast<const float4 *>(v + (int64_t)min(s_, T - 1) * ldv + h * kHD + c0);
 #pragma unroll
-                for (int c = 0; c < kHD; c++) acc[c] *= corr;
-                mx = d;
+            for (int j = 0; j < 4; j++) {
+                float4 a = kr[j], b = vr[j];
+                if (!in) a = b = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                Ks[wave][row][c0 + 4 * j + 0] = a.x;
+                Ks[wave][row][c0 + 4 * j + 1] = a.y;
+                Ks[wave][row][c0 + 4 * j + 2] = a.z;
+                Ks[wave][row][c0 + 4 * j + 3] = a.w;
+                Vs[wave][row][c0 + 4 * j + 0] = b.x;
+                Vs[wave][row][c0 + 4 * j + 1] = b.y;
+                Vs[wave][row][c0 + 4 * j + 2] = b.z;
+                Vs[wave][row][c0 + 4 * j + 3] = b.w;
             }
-            const float p = expf(d - mx);
-            l += p;
-#pragma unroll
-            for (int c = 0; c < kHD; c++) acc[c] = fmaf(p, Vs[r][c], acc[c]);
         }
+        __builtin_amdgcn_wave_barrier();
+        // S^T[key][q]: A = K (lane: key l32, d = 2st + hi)
+        f32x16_t sc;
+#pragma unroll
+        for (int r = 0; r < 16; r++) sc[r] = 0.0f;
+#pragma unroll
+        for (int st = 0; st < kHD / 2; st++)
+            sc = __builtin_amdgcn_mfma_f32_32x32x2f32(Ks[wave][l32][2 * st + hi], qf[st], sc, 0, 0, 0);
+        // scale, mask keys past T, chunk max per query (lane pair l32, l32 + 32)
+        float mx = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int key = key0 + 8 * (r >> 2) + 4 * hi + (r & 3);
+            sc[r] = key < T ? sc[r] * scale : -INFINITY;
+            mx = fmaxf(mx, sc[r]);
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float mn = fmaxf(m, mx);  // finite: the chunk holds at least one key < T
+        const float corr = expf(m - mn);
+        float ps = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            sc[r] = expf(sc[r] - mn);
+            ps += sc[r];
+        }
+        ps += __shfl_xor(ps, 32);
+        lsum = lsum * corr + ps;
+        m = mn;
+#pragma unroll
+        for (int r = 0; r < 16; r++) o[r] *= corr;
+        // O^T[d][q] += V^T P^T: step st pairs keys 8(st/4) + st%4 (+4 in the upper half)
+#pragma unroll
+        for (int st = 0; st < 16; st++)
+            o = __builtin_amdgcn_mfma_f32_32x32x2f32(Vs[wave][8 * (st >> 2) + 4 * hi + (st & 3)][l32], sc[st], o, 0,
+                                                     0, 0);
+        __builtin_amdgcn_wave_barrier();
     }
-    red_m[qi][part] = mx;
-    red_l[qi][part] = l;
+
+    // merge the waves' partial softmaxes
+    if (hi == 0) {
+        mw[wave][l32] = m;
+        lw[wave][l32] = lsum;
+    }
 #pragma unroll
-    for (int c = 0; c < kHD; c++) red_o[qi][part][c] = acc[c];
+    for (int r = 0; r < 16; r++) ow[wave][8 * (r >> 2) + 4 * hi + (r & 3)][l32] = o[r];
     __syncthreads();
-    if (part == 0 && live) {
-        float m = red_m[qi][0];
-        for (int p = 1; p < 4; p++) m = fmaxf(m, red_m[qi][p]);
-        float L = 0.0f, w[4];
-        for (int p = 0; p < 4; p++) {
-            w[p] = red_m[qi][p] == -INFINITY ? 0.0f : expf(red_m[qi][p] - m);
-            L += w[p] * red_l[qi][p];
+    const int d = threadIdx.x & 31;
+#pragma unroll
+    for (int j = 0; j < kAttQ / 8; j++) {
+        const int qi = (threadIdx.x >> 5) + 8 * j, t = q0 + qi;
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < kAttWaves; w++) M = fmaxf(M, mw[w][qi]);
+        float L = 0.0f, acc = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kAttWaves; w++) {
+            const float e = mw[w][qi] == -INFINITY ? 0.0f : expf(mw[w][qi] - M);
+            L += e * lw[w][qi];
+            acc += e * ow[w][d][qi];
         }
-        for (int c = 0; c < kHD; c++) {
-            float o = 0.0f;
-            for (int p = 0; p < 4; p++) o += w[p] * red_o[qi][p][c];
-            out[(int64_t)t * ldo + h * kHD + c] = o / L;
-        }
+        if (t < T) out[(int64_t)t * ldo + h * kHD + d] = acc / L;
     }
 }
 
@@ -322,6 +374,8 @@ hipError_t layernorm(const float *a, const float *b, const float *gamma, const f
 
 hipError_t attention(const float *q, int ldq, const float *k, int ldk, const float *v, int ldv, float *out,
                      int ldo, int T, hipStream_t s) {
+    // K and V rows are read as float4
+    if (T < 1 || ldk % 4 || ldv % 4 || (((uintptr_t)k | (uintptr_t)v) & 15)) return hipErrorInvalidValue;
     hipLaunchKernelGGL(k_attention, dim3((T + kAttQ - 1) / kAttQ, kNH), dim3(256), 0, s, q, ldq, k, ldk, v, ldv,
                        out, ldo, T, 1.0f / sqrtf((float)kHD));
     return hipGetLastError();

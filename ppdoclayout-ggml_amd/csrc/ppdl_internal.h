@@ -82,9 +82,9 @@ struct GemmPlan {
     int splits;  // split-K factor (1 = none)
 };
 
-GemmPlan gemm_plan(const GemmArgs &g, int64_t ws_bytes);
+GemmPlan gemm_plan(const GemmArgs &g, int64_t ws_bytes, bool im2col);
 int64_t gemm_ws_bytes(int M, int N, int batch, int cfg, int splits);
-int64_t gemm_ws_bytes_for(const GemmArgs &g);  // workspace the unconstrained plan uses
+int64_t gemm_ws_bytes_for(const GemmArgs &g, bool im2col);  // workspace the unconstrained plan uses
 hipError_t gemm_dense(const GemmArgs &g, const GemmWorkspace &ws, hipStream_t s);
 hipError_t gemm_im2col(const GemmArgs &g, const GemmWorkspace &ws, hipStream_t s);
 
@@ -107,6 +107,8 @@ hipError_t im2col_ggml(const float *x, float *dst, int64_t IW, int64_t IH, int64
 hipError_t msdeform(const float *val, const float *off, const float *awr, const float *ref,
                     float *out, int nq, hipStream_t s);
 hipError_t mask_box(const float *ml, float *out, int nq, hipStream_t s);
-hipError_t topk(const float *logits, int32_t *out, int ntok, int nc, int nq, hipStream_t s);
+// ws (optional, >= 8 * ntok bytes): per-token keys, computed grid-wide first
+hipError_t topk(const float *logits, int32_t *out, int ntok, int nc, int nq, void *ws, int64_t ws_bytes,
+                hipStream_t s);
 
 }  // namespace ppdl

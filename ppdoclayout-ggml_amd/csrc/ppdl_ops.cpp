@@ -57,6 +57,7 @@ int ws_index(const int32_t *p) {
         case PPDL_OP_CONV_IM2COL: return 3;
         case PPDL_OP_CONV1X1_BA: return p[15] ? 4 : 3;
         case PPDL_OP_WG4_MADD: return 2;
+        case PPDL_OP_TOPK: return 1;
         default: return -1;
     }
 }
@@ -282,10 +283,11 @@ extern "C" PPDL_HIP_API int64_t ppdl_hip_workspace_bytes(const int32_t op_params
     const int wi = ws_index(op_params);
     const int n = (wi >= 0 && nsrc > wi) ? wi : nsrc;  // ignore a workspace already attached
     if (check_op(op_params, dst, src, n) != PPDL_OK) return -1;
+    if (op_params[13] == PPDL_OP_TOPK) return src[0].ne[1] * 8;  // one 64-bit key per token
     GemmArgs g;
     bool im2col;
     if (!gemm_args_of(op_params, dst, src, &g, &im2col)) return 0;
-    return gemm_ws_bytes_for(g);
+    return gemm_ws_bytes_for(g, im2col);
 }
 
 extern "C" PPDL_HIP_API int ppdl_hip_supports(const int32_t op_params[16], const ppdl_tview *dst,
@@ -346,9 +348,11 @@ extern "C" PPDL_HIP_API int ppdl_hip_run(const int32_t op_params[16], const ppdl
                                       (float *)dst->data, (int)dst->ne[1], s));
         case PPDL_OP_MASKBOX:
             return status_of(mask_box((const float *)src[0].data, (float *)dst->data, (int)dst->ne[1], s));
-        case PPDL_OP_TOPK:
+        case PPDL_OP_TOPK: {
+            const GemmWorkspace ws = ws_of(p, src, nsrc);
             return status_of(topk((const float *)src[0].data, (int32_t *)dst->data, (int)src[0].ne[1],
-                                  (int)src[0].ne[0], (int)dst->ne[0], s));
+                                  (int)src[0].ne[0], (int)dst->ne[0], ws.base, ws.bytes, s));
+        }
         default:
             return PPDL_UNSUPPORTED;
     }

@@ -143,6 +143,27 @@ def test_conv1x1_shapes(hip, orc, IC, H, W, OC, act):
     assert normwise(y, orc.conv2d_f64(x, w, b, 1, 0, act)) < TOL
 
 
+@pytest.mark.parametrize("IC,H,W,OC", [
+    (1, 1, 1, 1), (3, 7, 5, 2), (17, 13, 11, 33), (256, 15, 20, 256), (1024, 17, 19, 96), (70, 9, 9, 300),
+])
+def test_small_gemm_kernel(hip, orc, IC, H, W, OC, monkeypatch):
+    """The small-GEMM kernel (32x32 tiles, K split over the block's waves)
+    forced for every GEMM, on edge shapes: K not a multiple of the 64-wide
+    chunk, fewer chunks than waves, M and N not multiples of 32."""
+    monkeypatch.setenv("PPDL_GEMM_TILE", "6,1")
+    say(f"small GEMM 1x1 {IC}->{OC} @{H}x{W}")
+    rng = np.random.default_rng(IC + 3 * OC + H)
+    x, w, b = conv_inputs(rng, IC, H, W, OC, 1)
+    out, _ = hip_conv1x1(hip, x, w, b, 2)
+    y = host(out)
+    assert normwise(y, orc.conv2d_ref(x, w, b, 1, 0, 2)) < TOL
+    # Winograd planes through the same kernel (batch 36)
+    if IC <= 256 and H >= 5:
+        x3, w3, b3 = conv_inputs(rng, IC, H, W, OC, 3)
+        wo = hip_winograd(hip, x3, w3, b3, 1)[0]
+        assert normwise(host(wo), orc.conv2d_ref(x3, w3, b3, 1, 1, 1)) < TOL
+
+
 # ---------------------------------------------------------------- Winograd F(4,3)
 WG_CONFIGS = [(256, 100, 100), (256, 50, 50), (256, 25, 25), (48, 200, 200), (96, 100, 100)]
 
@@ -391,24 +412,33 @@ def test_mask_box(hip, orc):
     assert rel1(y, ref) < 1e-6
 
 
-def test_topk(hip, orc):
+@pytest.mark.parametrize("with_ws", [False, True])
+def test_topk(hip, orc, with_ws):
+    """Both paths: keys computed by the selection block (no workspace) and by
+    the grid-wide key kernel (workspace of 8 bytes per token)."""
     rng = np.random.default_rng(22)
+    ws = torch.empty((13125 * 2,), dtype=torch.float32, device="cuda") if with_ws else None
+
+    def run(lg, nq):
+        out = torch.empty((nq,), dtype=torch.int32, device="cuda")
+        hip.run_checked(hip.OP_TOPK, out, [dev(lg)] + ([ws] if with_ws else []))
+        return host(out)
+
     lg = rng.standard_normal((13125, 25)).astype(np.float32)
     lg[10:20] = 9.0          # ties -> lower index first
     lg[7000, 3] = 9.0
     lg[40] = -0.0            # -0 and +0 compare equal
     lg[41] = 0.0
-    out = torch.empty((300,), dtype=torch.int32, device="cuda")
-    hip.run_checked(hip.OP_TOPK, out, [dev(lg)])
-    assert np.array_equal(host(out), orc.topk(lg, 300))
-    # all equal -> 0..299
+    assert np.array_equal(run(lg, 300), orc.topk(lg, 300))
+    # all equal -> 0..299 (the selection runs into the index bytes)
     eq = np.zeros((13125, 25), np.float32)
-    hip.run_checked(hip.OP_TOPK, out, [dev(eq)])
-    assert np.array_equal(host(out), np.arange(300, dtype=np.int32))
+    assert np.array_equal(run(eq, 300), np.arange(300, dtype=np.int32))
+    # a tie group straddling the 300th place
+    tie = rng.standard_normal((13125, 25)).astype(np.float32)
+    tie[::37] = 5.0
+    assert np.array_equal(run(tie, 300), orc.topk(tie, 300))
     small = rng.standard_normal((50, 3)).astype(np.float32)
-    o2 = torch.empty((50,), dtype=torch.int32, device="cuda")
-    hip.run_checked(hip.OP_TOPK, o2, [dev(small)])
-    assert np.array_equal(host(o2), orc.topk(small, 50))
+    assert np.array_equal(run(small, 50), orc.topk(small, 50))
 
 
 # ---------------------------------------------------------------- graph capture
