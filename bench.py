@@ -1,26 +1,33 @@
-"""Benchmark of the tagged-op hot path on one MI355X.
+"""Benchmark of PP-DocLayoutV3 inference on one MI355X.
 
-Workload "conv_suite": one step is one hipGraph replay of the BASELINE op
-configs at their real shapes, all through the C-ABI:
-  1x1 512->256 @100^2 + ReLU; the F(4,3) sweep (256 @100/50/25, 48 @200,
-  96 @100, SiLU); the im2col convs (k2 48->24 @401, k3s2 256 @100 and @50,
-  k3s2 3->32 @800); MSDeformAttn at 300 queries.
-The headline metric's first half (ms/image of the full network) needs the
-whole PP-DocLayoutV3 graph; this workload reports its second half: conv GEMM
-TFLOPS as a percentage of the FP32 matrix peak, summed over the suite's conv
-GEMM kernels (Winograd counted at its 36-plane GEMM FLOPs).
+Default workload "network": the full PP-DocLayoutV3 graph at 800x800 (HGNetV2
+backbone, hybrid encoder, 6-layer deformable decoder, heads) with seeded
+random-init FP32 weights of that architecture written as a GGUF, on a
+synthetic document page.  One step is one hipGraph replay of the whole graph
+(the span the reference reports as infer_ms: no host copies).  `value` is the
+device time per image from HIP events on the replay stream.
 
-Timing: W untimed warm-up replays, then K replays between
-torch.cuda.synchronize() (and HIP events on the replay stream).  Per-kernel
-times come from HIP events around repeated launches of each node on the
-stream it is launched on.  The CPU baseline is the oracle's restatement of
-the reference CPU path (im2col + FP32 GEMM convs, the msdeform loop) on the
-host cores, over a bounded number of suite passes.
+The metric's second half, conv GEMM TFLOPS as a fraction of the FP32 matrix
+peak, comes from the per-node profile (ppdl_profile_nodes: every node run
+eagerly between HIP events on the graph's stream): algorithmic conv GEMM FLOP
+(Winograd counted at its 36-plane GEMM) over the conv GEMM nodes' time.
+
+roofline: the GEMM kernel with the largest total time in one image, its
+algorithmic FLOP per launch over its mean launch time; traffic is its HBM
+bytes per launch from the committed rocprofv3 --pmc summary.
+
+cpu_baseline: the oracle's restatement of the reference CPU path (im2col +
+FP32 GEMM convs, the stock ops in numpy) on the same weights and image, timed
+on the host over a bounded number of images.
+
+Workload "conv_suite": the single-op configurations (1x1 512->256 @100^2,
+the F(4,3) sweep, the im2col convs, MSDeformAttn) as one hipGraph.
 """
 import argparse
 import json
 import os
 import sys
+import tempfile
 import time
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
@@ -32,11 +39,174 @@ for _p in (ROOT, PKG):
 PEAK_FP32_MFMA_TFLOPS = 157.3
 PEAK_HBM_GBPS = 8000.0
 METRIC = "ms/image @800×800 FP32 (hipGraph); conv GEMM TFLOPS as % of FP32 MFMA peak"
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "network_traffic.json")
+SUITE_TRAFFIC_FILE = os.path.join(ROOT, "profiles", "conv_suite_traffic.json")
 
 
+def sync():
+    try:
+        import torch
+
+        if torch.cuda.is_available():
+            torch.cuda.synchronize()
+    except ImportError:
+        pass
+
+
+def measured_traffic(path, key):
+    """HBM bytes per launch (FETCH_SIZE + WRITE_SIZE, copy-calibrated) of
+    `key` from a committed rocprofv3 summary, or (None, None)."""
+    try:
+        with open(path) as f:
+            rec = json.load(f)["kernels"].get(key)
+    except (OSError, ValueError, KeyError):
+        return None, None
+    if not rec:
+        return None, None
+    return rec["bytes"], os.path.relpath(path, ROOT) + " (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE)"
+
+
+def calib_copy(mib):
+    """A plain elementwise copy of known size: reads and writes exactly `mib`
+    MiB, the scale for the HBM byte counters of a --pmc run."""
+    import torch
+
+    n = mib * (1 << 20) // 4
+    a = torch.ones(n, device="cuda")
+    b = torch.empty_like(a)
+    for _ in range(3):
+        torch.mul(a, 1.0, out=b)
+    torch.cuda.synchronize()
+
+
+# ---------------------------------------------------------------- network
+def network_cpu_baseline(weights, image, budget_s):
+    from oracle import ppdl_net
+
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or (os.cpu_count() or 1)
+    net = ppdl_net.Net(weights, threads=threads)
+    n, t0 = 0, time.perf_counter()
+    while True:
+        net.forward(image)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or n >= 20:
+            break
+    return el * 1000.0 / n, n, threads
+
+
+def run_network(args):
+    import ppdoclayout as P
+    import synth_gguf
+    from oracle import ppdl_net
+
+    tmp = tempfile.mkdtemp(prefix="ppdl_bench_")
+    path = os.path.join(tmp, "ppdlv3-random-seed0.gguf")
+    weights = synth_gguf.write_random_model(path, seed=0)
+    image = ppdl_net.doc_image(0)
+    ctx = P.PPDocLayout(path, P.BACKEND_HIP)
+    launches = ctx.graph_nodes()
+    ctx.compute(image)  # uploads the page (resident from here on) and replays once
+
+    if args.warmup > 0:
+        ctx.time_graph(args.warmup)
+    sync()
+    t0 = time.perf_counter()
+    ms = ctx.time_graph(args.steps)  # HIP events around `steps` replays on the graph's stream
+    sync()
+    wall_ms = (time.perf_counter() - t0) * 1000.0 / args.steps
+
+    nodes = ctx.profile_nodes(args.kernel_reps)
+    if args.calib_copy_mib > 0:
+        calib_copy(args.calib_copy_mib)
+    ctx.close()
+
+    conv = [n for n in nodes if n["cls"] == P.NODE_CONV_GEMM]
+    lin = [n for n in nodes if n["cls"] == P.NODE_LINEAR_GEMM]
+    conv_fl, conv_us = sum(n["flops"] for n in conv), sum(n["us"] for n in conv)
+    lin_fl, lin_us = sum(n["flops"] for n in lin), sum(n["us"] for n in lin)
+    conv_tf = conv_fl / (conv_us * 1e-6) / 1e12
+    lin_tf = lin_fl / (lin_us * 1e-6) / 1e12
+
+    # dominant GEMM kernel: largest total time over the single-kernel GEMM nodes
+    groups = {}
+    for n in conv + lin:
+        if n["kernels"] != 1:
+            continue
+        g = groups.setdefault(n["kernel"], {"us": 0.0, "flops": 0.0, "launches": 0})
+        g["us"] += n["us"]
+        g["flops"] += n["flops"]
+        g["launches"] += 1
+    dom_name, dom = max(groups.items(), key=lambda kv: kv[1]["us"])
+    dom_us = dom["us"] / dom["launches"]
+    dom_fl = dom["flops"] / dom["launches"]
+    dom_tf = dom_fl / (dom_us * 1e-6) / 1e12
+    traffic, traffic_src = measured_traffic(TRAFFIC_FILE, dom_name)
+    roofline = {
+        "bound": "mfma",
+        "kernel": dom_name,
+        "achieved": round(dom_tf, 2),
+        "peak": PEAK_FP32_MFMA_TFLOPS,
+        "unit": "TFLOP/s",
+        "frac": round(dom_tf / PEAK_FP32_MFMA_TFLOPS, 4),
+        "traffic": traffic,
+        "traffic_source": traffic_src,
+        "flops_per_launch": round(dom_fl),
+        "us_per_launch": round(dom_us, 2),
+        "launches_per_image": dom["launches"],
+    }
+
+    cpu = None
+    if not args.no_cpu:
+        cpu_ms, n_img, cores = network_cpu_baseline(weights, image, args.cpu_budget)
+        cpu = {
+            "value": round(cpu_ms, 1),
+            "unit": "ms/image",
+            "cores": cores,
+            "kind": "port",
+            "sample": f"{n_img} full 800x800 images through the oracle's restatement of the reference CPU path "
+                      f"(im2col + FP32 GEMM convs in C, stock ops and linears in numpy), {cores} threads",
+        }
+
+    top = sorted(nodes, key=lambda n: -n["us"])[:12]
+    line = {
+        "metric": METRIC,
+        "value": round(ms, 4),
+        "unit": "ms/image",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "wall_ms_per_step": round(wall_ms, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic: seeded random-init FP32 weights of the PP-DocLayoutV3 architecture (GGUF), "
+                "synthetic 3x800x800 document page; inputs resident in HBM",
+        "config": {
+            "workload": "network: full PP-DocLayoutV3 @800x800 (HGNetV2-L backbone, hybrid encoder, 6-layer "
+                        "deformable decoder, class/box/mask/order heads) as one hipGraph replay",
+            "kernel_launches_per_image": launches,
+            "conv_gemm_tflops": round(conv_tf, 2),
+            "conv_gemm_pct_of_fp32_mfma_peak": round(100.0 * conv_tf / PEAK_FP32_MFMA_TFLOPS, 2),
+            "conv_gemm_gflop_per_image": round(conv_fl / 1e9, 3),
+            "conv_gemm_us_per_image": round(conv_us, 1),
+            "linear_gemm_tflops": round(lin_tf, 2),
+            "linear_gemm_gflop_per_image": round(lin_fl / 1e9, 3),
+            "node_us_sum": round(sum(n["us"] for n in nodes), 1),
+        },
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "top_nodes": [{"name": n["name"], "us": round(n["us"], 2), "kernel": n["kernel"]} for n in top],
+    }
+    return line
+
+
+# ---------------------------------------------------------------- op suite
 def time_nodes(suite, stream, reps):
-    """Average device time (us) of each node: `reps` back-to-back launches
-    between two HIP events recorded on the launch stream."""
+    """Average device time (us) of each suite node: `reps` back-to-back
+    launches between two HIP events recorded on the launch stream."""
     import torch
 
     out = {}
@@ -54,21 +224,7 @@ def time_nodes(suite, stream, reps):
     return out
 
 
-def measured_traffic(node):
-    """HBM bytes per launch of `node` (FETCH_SIZE + WRITE_SIZE, copy-calibrated)
-    from the committed rocprofv3 summary, or (None, None) if not profiled."""
-    path = os.path.join(ROOT, "profiles", "conv_suite_traffic.json")
-    try:
-        with open(path) as f:
-            rec = json.load(f)["nodes"].get(node)
-    except (OSError, ValueError, KeyError):
-        return None, None
-    if not rec:
-        return None, None
-    return rec["bytes"], "profiles/conv_suite_traffic.json (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE)"
-
-
-def cpu_baseline(budget_s):
+def suite_cpu_baseline(budget_s):
     """Suite passes through the oracle's reference CPU path until budget_s."""
     import numpy as np
 
@@ -79,21 +235,20 @@ def cpu_baseline(budget_s):
     cases = []
     x = rng.random((512, 100, 100)).astype(np.float32)
     w, b = workloads._conv_weights(rng, 512, 256, 1)
-    cases.append(("conv", x, w, b, 1, 0, 1))
+    cases.append((x, w, b, 1, 0, 1))
     for (C, Hh, W) in workloads.WINOGRAD_SWEEP:
         x = rng.random((C, Hh, W)).astype(np.float32)
         w, b = workloads._conv_weights(rng, C, C, 3)
-        cases.append(("conv", x, w, b, 1, 1, 2))
+        cases.append((x, w, b, 1, 1, 2))
     for (IC, IH, IW, OC, K, S, P) in workloads.IM2COL_CONVS:
         x = rng.random((IC, IH, IW)).astype(np.float32)
         w, b = workloads._conv_weights(rng, IC, OC, K)
-        cases.append(("conv", x, w, b, S, P, 0))
+        cases.append((x, w, b, S, P, 0))
     ms_in = workloads.msdef_inputs(rng)
     nthreads = os.cpu_count() or 1
     passes, t0 = 0, time.perf_counter()
     while True:
-        for c in cases:
-            _, x, w, b, S, P, act = c
+        for (x, w, b, S, P, act) in cases:
             oracle.conv2d_ref(x, w, b, S, P, act, nthreads)
         oracle.msdeform(*ms_in, nthreads)
         passes += 1
@@ -103,34 +258,15 @@ def cpu_baseline(budget_s):
     return el * 1000.0 / passes, passes, nthreads
 
 
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--kernel-reps", type=int, default=20)
-    ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU baseline work")
-    ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--calib-copy-mib", type=int, default=0,
-                    help="also run a plain copy of this many MiB (PMC byte-counter calibration)")
-    args = ap.parse_args()
-
-    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path (images are independent; "
-              "scale by running one process per GPU). Use --gpus 1.", file=sys.stderr)
-        sys.exit(2)
-
+def run_suite(args):
     import torch
 
     import ppdl_hip
     import workloads
 
-    torch.cuda.set_device(0)
     ppdl_hip.lib()
     suite = workloads.ConvSuite()
     stream = torch.cuda.Stream()
-
-    # capture one pass into a hipGraph
     with torch.cuda.stream(stream):
         suite.run(stream.cuda_stream)  # eager warm pass (also first-touch)
     stream.synchronize()
@@ -138,7 +274,6 @@ def main():
     with torch.cuda.graph(graph, stream=stream):
         suite.run(stream.cuda_stream)
     torch.cuda.synchronize()
-
     with torch.cuda.stream(stream):
         for _ in range(args.warmup):
             graph.replay()
@@ -154,22 +289,11 @@ def main():
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1000.0
     ms_per_step = e0.elapsed_time(e1) / args.steps
-
-    # per-kernel device times (HIP events on the launch stream)
     with torch.cuda.stream(stream):
         kt = time_nodes(suite, stream, args.kernel_reps)
     torch.cuda.synchronize()
-
     if args.calib_copy_mib > 0:
-        # a plain elementwise copy of known size: reads and writes exactly
-        # calib_copy_mib MiB, the scale for HBM byte counters
-        n = args.calib_copy_mib * (1 << 20) // 4
-        a = torch.ones(n, device="cuda")
-        b = torch.empty_like(a)
-        for _ in range(3):
-            torch.mul(a, 1.0, out=b)
-        torch.cuda.synchronize()
-        del a, b
+        calib_copy(args.calib_copy_mib)
 
     kernels = {}
     gemm_flops = gemm_us = 0.0
@@ -189,28 +313,17 @@ def main():
             rec.update(gbps=round(gbps, 1), frac=round(gbps / PEAK_HBM_GBPS, 4))
         kernels[n.name] = rec
     agg_tflops = gemm_flops / (gemm_us * 1e-6) / 1e12
-    value = 100.0 * agg_tflops / PEAK_FP32_MFMA_TFLOPS
-
     dom_us = kt[dominant.name]
     dom_tf = dominant.flops / (dom_us * 1e-6) / 1e12
-    traffic, traffic_src = measured_traffic(dominant.name)
-    roofline = {
-        "bound": "mfma",
-        "kernel": dominant.name,
-        "achieved": round(dom_tf, 2),
-        "peak": PEAK_FP32_MFMA_TFLOPS,
-        "unit": "TFLOP/s",
-        "frac": round(dom_tf / PEAK_FP32_MFMA_TFLOPS, 4),
-        "traffic": traffic,
-        "traffic_source": traffic_src,
-        "algorithmic_bytes": dominant.bytes,
-        "flops_per_launch": dominant.flops,
-        "us_per_launch": round(dom_us, 2),
-    }
-
+    try:
+        with open(SUITE_TRAFFIC_FILE) as f:
+            rec = json.load(f)["nodes"].get(dominant.name)
+        traffic = rec["bytes"] if rec else None
+    except (OSError, ValueError, KeyError):
+        traffic = None
     cpu = None
     if not args.no_cpu:
-        cpu_ms, passes, cores = cpu_baseline(args.cpu_budget)
+        cpu_ms, passes, cores = suite_cpu_baseline(args.cpu_budget)
         cpu = {
             "value": round(cpu_ms, 2),
             "unit": "ms/step",
@@ -219,13 +332,11 @@ def main():
             "sample": f"{passes} full passes of the same suite through the oracle's restatement of the "
                       f"reference CPU path (im2col + FP32 GEMM convs with bias/act, msdeform loop), "
                       f"{cores} OpenMP threads",
-            "gpu_ms_per_step": round(ms_per_step, 4),
         }
-
-    line = {
+    return {
         "metric": METRIC,
-        "value": round(value, 3),
-        "unit": "% of FP32 MFMA peak (conv GEMMs, 157.3 TFLOP/s)",
+        "value": round(100.0 * agg_tflops / PEAK_FP32_MFMA_TFLOPS, 3),
+        "unit": "% of FP32 MFMA peak (conv GEMMs of the op suite, 157.3 TFLOP/s)",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
@@ -237,16 +348,40 @@ def main():
         "dtype": "f32",
         "data": "synthetic (seeded U(0,1) activations, N(0,1/sqrt(fan_in)) weights)",
         "config": {
-            "workload": "conv_suite: BASELINE configs 1-4 (1x1 512->256@100^2; F(4,3) 256@100/50/25, "
-                        "48@200, 96@100; im2col k2 48->24@401, k3s2 256@100/@50, 3->32@800; "
-                        "MSDeformAttn 300q) as one hipGraph, 21 tagged-op launches per step",
+            "workload": "conv_suite: 1x1 512->256@100^2; F(4,3) 256@100/50/25, 48@200, 96@100; im2col k2 "
+                        "48->24@401, k3s2 256@100/@50, 3->32@800; MSDeformAttn 300q; one hipGraph, 21 launches",
             "conv_gemm_tflops": round(agg_tflops, 2),
             "conv_gemm_gflop_per_step": round(gemm_flops / 1e9, 3),
         },
-        "roofline": roofline,
+        "roofline": {
+            "bound": "mfma", "kernel": dominant.name, "achieved": round(dom_tf, 2),
+            "peak": PEAK_FP32_MFMA_TFLOPS, "unit": "TFLOP/s", "frac": round(dom_tf / PEAK_FP32_MFMA_TFLOPS, 4),
+            "traffic": traffic, "flops_per_launch": dominant.flops, "us_per_launch": round(dom_us, 2),
+        },
         "cpu_baseline": cpu,
         "kernels": kernels,
     }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", choices=["network", "conv_suite"], default="network")
+    ap.add_argument("--kernel-reps", type=int, default=10, help="eager runs per node in the per-node profile")
+    ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU baseline work")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--calib-copy-mib", type=int, default=0,
+                    help="also run a plain copy of this many MiB (PMC byte-counter calibration)")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (images are independent; "
+              "scale by running one process per GPU). Use --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    line = run_network(args) if args.workload == "network" else run_suite(args)
     print(json.dumps(line), flush=True)
 
 

@@ -82,6 +82,23 @@ PPDL_API double ppdl_time_graph(ppdl_ctx * ctx, int iters);
 /* Number of kernel nodes one graph replay executes (0 if not built). */
 PPDL_API int ppdl_graph_nodes(ppdl_ctx * ctx);
 
+/* Per-node device time of the graph: each node (one layer's kernels) is run
+ * eagerly `iters` times between two HIP events on the graph's stream. */
+typedef struct {
+    char    name[64];    /* layer / node name                                   */
+    char    kernel[64];  /* GEMM nodes: the device kernel(s) the plan launches   */
+    int32_t cls;         /* 0 other, 1 conv GEMM, 2 linear (token-major) GEMM    */
+    int32_t kernels;     /* kernel launches per run of the node                  */
+    double  flops;       /* GEMM nodes: algorithmic FLOP per run (Winograd: the
+                            36-plane GEMM), else 0                               */
+    double  us;          /* mean device time per run, microseconds              */
+} ppdl_node_stat;
+
+/* Fills out[0..n) for the first min(cap, nodes) nodes; returns n or -1.
+ * Intermediate buffers are left in an arbitrary state (the next ppdl_infer or
+ * ppdl_compute recomputes them). */
+PPDL_API int ppdl_profile_nodes(ppdl_ctx * ctx, int iters, ppdl_node_stat * out, int cap);
+
 #ifdef __cplusplus
 }
 #endif

@@ -30,6 +30,7 @@
 //
 // No TF32/bf16 emulation anywhere: products and accumulation are IEEE fp32 in
 // the matrix core; split partials are summed in fp32.
+#include <cstdio>
 #include <cstdlib>
 #include <type_traits>
 
@@ -744,6 +745,17 @@ int64_t gemm_ws_bytes_for(const GemmArgs &g, bool im2col) {
 }
 
 hipError_t gemm_dense(const GemmArgs &g, const GemmWorkspace &ws, hipStream_t s) { return dispatch<0>(g, ws, s); }
+
+std::string gemm_kernel_name(const GemmArgs &g, int64_t ws_bytes, bool im2col) {
+    const GemmPlan p = gemm_plan(g, ws_bytes, im2col);
+    if (p.cfg == kCfgSmall) return g.a_rowmajor ? "k_gemm_small<1>" : "k_gemm_small<0>";
+    int bm = kCfgs[p.cfg].bm, bn = kCfgs[p.cfg].bn, wgm = kCfgs[p.cfg].wgm;
+    if (g.a_rowmajor && p.cfg != 5) bm = 64, bn = 64, wgm = 2;  // the two row-major-A shapes
+    char buf[96];
+    snprintf(buf, sizeof(buf), "k_gemm<%d, %d, %d, %d, %d, %s>%s", bm, bn, wgm, g.a_rowmajor ? 1 : 0, im2col ? 1 : 0,
+             p.splits > 1 ? "true" : "false", p.splits > 1 ? "+k_splitk_reduce" : "");
+    return buf;
+}
 hipError_t gemm_im2col(const GemmArgs &g, const GemmWorkspace &ws, hipStream_t s) { return dispatch<1>(g, ws, s); }
 
 }  // namespace ppdl

@@ -50,6 +50,9 @@ struct Node {
     std::string name;
     int kernels;  // device kernels this node launches
     std::function<int(hipStream_t)> run;
+    int cls = 0;         // 0 other, 1 conv GEMM, 2 linear GEMM
+    double flops = 0.0;  // algorithmic GEMM FLOP per run
+    std::string kern;    // GEMM kernel(s) the node's plan launches
 };
 
 struct DumpRec {
@@ -104,6 +107,7 @@ class Net {
     bool capture(std::string *err);
     int replay();  // one graph launch + sync
     double time_graph(int iters);
+    int profile_nodes(int iters, ppdl_node_stat *out, int cap);
     bool upload_image(const float *host);
 
     int nodes() const {
@@ -159,6 +163,13 @@ class Net {
     void node(const std::string &name, int kernels, std::function<int(hipStream_t)> fn) {
         nodes_.push_back({name, kernels, std::move(fn)});
     }
+    // GEMM bookkeeping of the node just emitted (for ppdl_profile_nodes)
+    void gemm_meta(int cls, const GemmArgs &g, int64_t ws_bytes, bool im2col) {
+        Node &n = nodes_.back();
+        n.cls = cls;
+        n.flops = 2.0 * g.M * (double)g.N * g.K * g.batch;
+        n.kern = gemm_kernel_name(g, ws_bytes, im2col);
+    }
     // one tagged op through the C-ABI; a GEMM op gets the shared split-K
     // workspace appended when its plan asks for one
     void tagged(const std::string &name, int op, int p14, int p15, ppdl_tview dst, std::vector<ppdl_tview> src) {
@@ -175,6 +186,9 @@ class Net {
             if (wsb > 0) sv.push_back(view(ws_, {(ws_bytes_ + 3) / 4}));
             return ppdl_hip_run(pv.data(), &dst, sv.data(), (int)sv.size(), s);
         });
+        GemmArgs g;
+        bool im2col;
+        if (gemm_args_of(pv.data(), &dst, src.data(), &g, &im2col)) gemm_meta(1, g, wsb, im2col);
     }
     void gemm(const std::string &name, GemmArgs g) {
         const int64_t wsb = gemm_ws_bytes_for(g, false);
@@ -183,6 +197,7 @@ class Net {
             GemmWorkspace ws{wsb > 0 ? ws_ : nullptr, wsb > 0 ? ws_bytes_ : 0};
             return gemm_dense(g, ws, s) == hipSuccess ? 0 : 3;
         });
+        gemm_meta(2, g, wsb, false);
     }
     static int ok(hipError_t e) { return e == hipSuccess ? 0 : 3; }
 
@@ -336,6 +351,11 @@ Img Net::conv(const Img &x, const std::string &name, int s, int p, int act, floa
             if (wsb > 0) sv.push_back(view(ws_, {(ws_bytes_ + 3) / 4}));
             return ppdl_hip_run(p_md.data(), &d, sv.data(), (int)sv.size(), st);
         });
+        {
+            GemmArgs g;
+            bool im2col;
+            if (gemm_args_of(p_md.data(), &qd, qs, &g, &im2col)) gemm_meta(1, g, wsb, im2col);
+        }
         node(name + ".wg_out", 1, [=](hipStream_t st) {
             ppdl_tview d = view(y);
             ppdl_tview sv[2] = {view(wg_yt_, {T, OC, 36}), view(b, {OC})};
@@ -771,6 +791,41 @@ double Net::time_graph(int iters) {
     return good ? (double)ms / iters : -1.0;
 }
 
+// Each node run eagerly `iters` times between two HIP events on the graph's
+// stream (after two untimed runs): the per-node device time the graph is made
+// of.  Nodes that update a buffer in place drift its contents meanwhile; the
+// next ppdl_infer / ppdl_compute recomputes everything from the image.
+int Net::profile_nodes(int iters, ppdl_node_stat *out, int cap) {
+    hipEvent_t e0, e1;
+    if (iters < 1 || hipEventCreate(&e0) != hipSuccess) return -1;
+    if (hipEventCreate(&e1) != hipSuccess) {
+        (void)hipEventDestroy(e0);
+        return -1;
+    }
+    int n = 0;
+    bool good = true;
+    for (size_t i = 0; good && i < nodes_.size() && n < cap; i++) {
+        Node &nd = nodes_[i];
+        for (int r = 0; good && r < 2; r++) good = nd.run(stream_) == 0;
+        good = good && hipEventRecord(e0, stream_) == hipSuccess;
+        for (int r = 0; good && r < iters; r++) good = nd.run(stream_) == 0;
+        good = good && hipEventRecord(e1, stream_) == hipSuccess && hipEventSynchronize(e1) == hipSuccess;
+        float ms = 0.0f;
+        good = good && hipEventElapsedTime(&ms, e0, e1) == hipSuccess;
+        ppdl_node_stat &o = out[n++];
+        memset(&o, 0, sizeof(o));
+        snprintf(o.name, sizeof(o.name), "%s", nd.name.c_str());
+        snprintf(o.kernel, sizeof(o.kernel), "%s", nd.kern.c_str());
+        o.cls = nd.cls;
+        o.kernels = nd.kernels;
+        o.flops = nd.flops;
+        o.us = 1000.0 * ms / iters;
+    }
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    return good ? n : -1;
+}
+
 // ---------------------------------------------------------------------------
 // Postprocess (src/ppdoclayout.cpp:927-993), on the host: reading-order votes,
 // top-300 over the 7500 class scores, box restore to the original size, mask
@@ -998,3 +1053,8 @@ extern "C" PPDL_API double ppdl_time_graph(ppdl_ctx *c, int iters) {
 }
 
 extern "C" PPDL_API int ppdl_graph_nodes(ppdl_ctx *c) { return c ? c->net->nodes() : 0; }
+
+extern "C" PPDL_API int ppdl_profile_nodes(ppdl_ctx *c, int iters, ppdl_node_stat *out, int cap) {
+    if (!c || !out || cap < 1) return -1;
+    return c->net->profile_nodes(iters, out, cap);
+}

@@ -2,7 +2,10 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <string>
 #include <stdint.h>
+
+#include "../../include/ppdl_hip_ops.h"
 
 namespace ppdl {
 
@@ -86,6 +89,10 @@ GemmPlan gemm_plan(const GemmArgs &g, int64_t ws_bytes, bool im2col);
 int64_t gemm_ws_bytes(int M, int N, int batch, int cfg, int splits);
 int64_t gemm_ws_bytes_for(const GemmArgs &g, bool im2col);  // workspace the unconstrained plan uses
 hipError_t gemm_dense(const GemmArgs &g, const GemmWorkspace &ws, hipStream_t s);
+// the kernel(s) the plan for g launches, named as the device symbols
+std::string gemm_kernel_name(const GemmArgs &g, int64_t ws_bytes, bool im2col);
+// GEMM description of a validated conv / madd tagged node (ppdl_ops.cpp)
+bool gemm_args_of(const int32_t *p, const ppdl_tview *dst, const ppdl_tview *src, GemmArgs *g, bool *im2col);
 hipError_t gemm_im2col(const GemmArgs &g, const GemmWorkspace &ws, hipStream_t s);
 
 // ---- Winograd transforms ----

@@ -201,7 +201,7 @@ int check_op(const int32_t *p, const ppdl_tview *dst, const ppdl_tview *src, int
 
 // GEMM description of a validated conv/madd node.  Returns false for ops that
 // are not GEMMs.  *im2col selects the implicit-im2col B operand.
-bool gemm_args_of(const int32_t *p, const ppdl_tview *dst, const ppdl_tview *src, GemmArgs *g, bool *im2col) {
+bool args_of_node(const int32_t *p, const ppdl_tview *dst, const ppdl_tview *src, GemmArgs *g, bool *im2col) {
     *g = GemmArgs{};
     *im2col = false;
     switch (p[13]) {
@@ -275,6 +275,10 @@ bool gemm_args_of(const int32_t *p, const ppdl_tview *dst, const ppdl_tview *src
 
 }  // namespace
 
+bool ppdl::gemm_args_of(const int32_t *p, const ppdl_tview *dst, const ppdl_tview *src, GemmArgs *g, bool *im2col) {
+    return args_of_node(p, dst, src, g, im2col);
+}
+
 extern "C" PPDL_HIP_API int64_t ppdl_hip_workspace_bytes(const int32_t op_params[16], const ppdl_tview *dst,
                                                          const ppdl_tview *src, int nsrc) {
     if (!op_params || (uint32_t)op_params[12] != (uint32_t)PPDL_MAGIC || !dst || nsrc < 0 ||
@@ -286,7 +290,7 @@ extern "C" PPDL_HIP_API int64_t ppdl_hip_workspace_bytes(const int32_t op_params
     if (op_params[13] == PPDL_OP_TOPK) return src[0].ne[1] * 8;  // one 64-bit key per token
     GemmArgs g;
     bool im2col;
-    if (!gemm_args_of(op_params, dst, src, &g, &im2col)) return 0;
+    if (!args_of_node(op_params, dst, src, &g, &im2col)) return 0;
     return gemm_ws_bytes_for(g, im2col);
 }
 
@@ -317,7 +321,7 @@ extern "C" PPDL_HIP_API int ppdl_hip_run(const int32_t op_params[16], const ppdl
 
     GemmArgs g;
     bool im2col;
-    if (gemm_args_of(p, dst, src, &g, &im2col)) {
+    if (args_of_node(p, dst, src, &g, &im2col)) {
         const GemmWorkspace ws = ws_of(p, src, nsrc);
         return status_of(im2col ? gemm_im2col(g, ws, s) : gemm_dense(g, ws, s));
     }

@@ -40,6 +40,7 @@ EXPORTS = (
     "ppdl_compute",
     "ppdl_time_graph",
     "ppdl_graph_nodes",
+    "ppdl_profile_nodes",
 )
 
 
@@ -51,6 +52,19 @@ class Result(ctypes.Structure):
         ("infer_ms", ctypes.c_double),
     ]
 
+
+class NodeStat(ctypes.Structure):
+    _fields_ = [
+        ("name", ctypes.c_char * 64),
+        ("kernel", ctypes.c_char * 64),
+        ("cls", ctypes.c_int32),
+        ("kernels", ctypes.c_int32),
+        ("flops", ctypes.c_double),
+        ("us", ctypes.c_double),
+    ]
+
+
+NODE_OTHER, NODE_CONV_GEMM, NODE_LINEAR_GEMM = 0, 1, 2
 
 _bound = None
 
@@ -80,6 +94,8 @@ def lib():
         L.ppdl_time_graph.restype = ctypes.c_double
         L.ppdl_graph_nodes.argtypes = [vp]
         L.ppdl_graph_nodes.restype = i32
+        L.ppdl_profile_nodes.argtypes = [vp, i32, ctypes.POINTER(NodeStat), i32]
+        L.ppdl_profile_nodes.restype = i32
         _bound = L
     return _bound
 
@@ -142,6 +158,16 @@ class PPDocLayout:
         if n != out.size:
             raise ppdl_hip.PpdlError("ppdl_get_raw(%d) returned %d" % (which, n))
         return out
+
+    def profile_nodes(self, iters):
+        """[dict(name, kernel, cls, kernels, flops, us)] per graph node."""
+        cap = 4096
+        arr = (NodeStat * cap)()
+        n = self._L.ppdl_profile_nodes(self._ctx, int(iters), arr, cap)
+        if n < 0:
+            raise ppdl_hip.PpdlError("ppdl_profile_nodes failed")
+        return [dict(name=a.name.decode(), kernel=a.kernel.decode(), cls=a.cls, kernels=a.kernels, flops=a.flops,
+                     us=a.us) for a in arr[:n]]
 
     def time_graph(self, iters):
         ms = self._L.ppdl_time_graph(self._ctx, int(iters))
