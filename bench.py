@@ -43,14 +43,53 @@ TRAFFIC_FILE = os.path.join(ROOT, "profiles", "network_traffic.json")
 SUITE_TRAFFIC_FILE = os.path.join(ROOT, "profiles", "conv_suite_traffic.json")
 
 
-def sync():
-    try:
-        import torch
+_HIP = None
 
-        if torch.cuda.is_available():
-            torch.cuda.synchronize()
-    except ImportError:
-        pass
+
+def hip_rt():
+    """libamdhip64 through ctypes: the network path needs device sync and one
+    plain copy, and touches no torch (the library owns the HIP context)."""
+    global _HIP
+    if _HIP is None:
+        import ctypes
+
+        for name in ("libamdhip64.so", "/opt/rocm/lib/libamdhip64.so"):
+            try:
+                _HIP = ctypes.CDLL(name)
+                break
+            except OSError:
+                continue
+        if _HIP is None:
+            raise RuntimeError("libamdhip64.so not found")
+        _HIP.hipMalloc.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_size_t]
+        _HIP.hipFree.argtypes = [ctypes.c_void_p]
+        _HIP.hipMemset.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t]
+        _HIP.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+    return _HIP
+
+
+def sync():
+    if hip_rt().hipDeviceSynchronize() != 0:
+        raise RuntimeError("hipDeviceSynchronize failed")
+
+
+def calib_copy_hip(mib):
+    """A plain device-to-device copy of `mib` MiB (the runtime's blit kernel
+    reads and writes exactly that many bytes): the scale for the HBM byte
+    counters of a --pmc run."""
+    import ctypes
+
+    h = hip_rt()
+    n = mib * (1 << 20)
+    a, b = ctypes.c_void_p(), ctypes.c_void_p()
+    if h.hipMalloc(ctypes.byref(a), n) or h.hipMalloc(ctypes.byref(b), n):
+        raise RuntimeError("hipMalloc failed")
+    h.hipMemset(a, 0, n)
+    for _ in range(3):
+        h.hipMemcpy(b, a, n, 3)  # hipMemcpyDeviceToDevice
+    sync()
+    h.hipFree(a)
+    h.hipFree(b)
 
 
 def measured_traffic(path, key):
@@ -118,7 +157,7 @@ def run_network(args):
 
     nodes = ctx.profile_nodes(args.kernel_reps)
     if args.calib_copy_mib > 0:
-        calib_copy(args.calib_copy_mib)
+        calib_copy_hip(args.calib_copy_mib)
     ctx.close()
 
     conv = [n for n in nodes if n["cls"] == P.NODE_CONV_GEMM]
@@ -133,9 +172,10 @@ def run_network(args):
     for n in conv + lin:
         if n["kernels"] != 1:
             continue
-        g = groups.setdefault(n["kernel"], {"us": 0.0, "flops": 0.0, "launches": 0})
+        g = groups.setdefault(n["kernel"], {"us": 0.0, "flops": 0.0, "bytes": 0.0, "launches": 0})
         g["us"] += n["us"]
         g["flops"] += n["flops"]
+        g["bytes"] += n["bytes"]
         g["launches"] += 1
     dom_name, dom = max(groups.items(), key=lambda kv: kv[1]["us"])
     dom_us = dom["us"] / dom["launches"]
@@ -152,6 +192,7 @@ def run_network(args):
         "traffic": traffic,
         "traffic_source": traffic_src,
         "flops_per_launch": round(dom_fl),
+        "algorithmic_bytes_per_launch": round(dom["bytes"] / dom["launches"]),
         "us_per_launch": round(dom_us, 2),
         "launches_per_image": dom["launches"],
     }

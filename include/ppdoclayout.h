@@ -91,6 +91,8 @@ typedef struct {
     int32_t kernels;     /* kernel launches per run of the node                  */
     double  flops;       /* GEMM nodes: algorithmic FLOP per run (Winograd: the
                             36-plane GEMM), else 0                               */
+    double  bytes;       /* GEMM nodes: compulsory HBM bytes per run (A, B and C
+                            once each), else 0                                   */
     double  us;          /* mean device time per run, microseconds              */
 } ppdl_node_stat;
 

@@ -52,6 +52,7 @@ struct Node {
     std::function<int(hipStream_t)> run;
     int cls = 0;         // 0 other, 1 conv GEMM, 2 linear GEMM
     double flops = 0.0;  // algorithmic GEMM FLOP per run
+    double bytes = 0.0;  // compulsory GEMM operand bytes per run
     std::string kern;    // GEMM kernel(s) the node's plan launches
 };
 
@@ -168,6 +169,9 @@ class Net {
         Node &n = nodes_.back();
         n.cls = cls;
         n.flops = 2.0 * g.M * (double)g.N * g.K * g.batch;
+        // the implicit-im2col B is the input image, read once
+        const double b_elems = im2col ? (double)g.IC * g.IH * g.IW : (double)g.K * g.N;
+        n.bytes = 4.0 * g.batch * ((double)g.M * g.K + b_elems + (double)g.M * g.N);
         n.kern = gemm_kernel_name(g, ws_bytes, im2col);
     }
     // one tagged op through the C-ABI; a GEMM op gets the shared split-K
@@ -819,6 +823,7 @@ int Net::profile_nodes(int iters, ppdl_node_stat *out, int cap) {
         o.cls = nd.cls;
         o.kernels = nd.kernels;
         o.flops = nd.flops;
+        o.bytes = nd.bytes;
         o.us = 1000.0 * ms / iters;
     }
     (void)hipEventDestroy(e0);

@@ -60,6 +60,7 @@ class NodeStat(ctypes.Structure):
         ("cls", ctypes.c_int32),
         ("kernels", ctypes.c_int32),
         ("flops", ctypes.c_double),
+        ("bytes", ctypes.c_double),
         ("us", ctypes.c_double),
     ]
 
@@ -160,14 +161,14 @@ class PPDocLayout:
         return out
 
     def profile_nodes(self, iters):
-        """[dict(name, kernel, cls, kernels, flops, us)] per graph node."""
+        """[dict(name, kernel, cls, kernels, flops, bytes, us)] per graph node."""
         cap = 4096
         arr = (NodeStat * cap)()
         n = self._L.ppdl_profile_nodes(self._ctx, int(iters), arr, cap)
         if n < 0:
             raise ppdl_hip.PpdlError("ppdl_profile_nodes failed")
         return [dict(name=a.name.decode(), kernel=a.kernel.decode(), cls=a.cls, kernels=a.kernels, flops=a.flops,
-                     us=a.us) for a in arr[:n]]
+                     bytes=a.bytes, us=a.us) for a in arr[:n]]
 
     def time_graph(self, iters):
         ms = self._L.ppdl_time_graph(self._ctx, int(iters))
