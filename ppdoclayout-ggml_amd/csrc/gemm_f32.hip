@@ -204,8 +204,12 @@ __global__ __launch_bounds__(kThreads) void k_gemm(GemmArgs g, SplitArgs sp, int
     // applied when the stage is written to LDS.  That keeps a fixed number of
     // loads per stage with no use of their results before the store, so the
     // compiler waits for one stage while the next stays in flight.  The
-    // edge/interior choice is made once per block (EDGE): interior tiles load
-    // float4 rows, tiles crossing M or N load clamped scalars.
+    // edge/interior choice is made once per block (EDGE).  Float4 loads are
+    // used unless the tile crosses an M or N edge that is not a multiple of 4:
+    // with a 4-aligned edge a float4 is either wholly inside or wholly past
+    // it, and one past it is clamped to the last valid float4 (finite values
+    // in rows / columns the epilogue never stores).  Other edge tiles load
+    // clamped scalars.
     auto body = [&](auto edge_tag) {
         constexpr bool EDGE = decltype(edge_tag)::value;
         auto load = [&](St &r, int kt) {
@@ -216,7 +220,7 @@ __global__ __launch_bounds__(kThreads) void k_gemm(GemmArgs g, SplitArgs sp, int
                     const int k = min(k0 + ak + e * RA, K - 1);
                     const float *row = A + (uint32_t)(k * lda);
                     if (!EDGE) {
-                        r.a[e] = ld4(row + gm);
+                        r.a[e] = ld4(row + min(gm, M - 4));
                     } else {
                         r.a[e].x = row[min(gm + 0, M - 1)];
                         r.a[e].y = row[min(gm + 1, M - 1)];
@@ -240,7 +244,7 @@ __global__ __launch_bounds__(kThreads) void k_gemm(GemmArgs g, SplitArgs sp, int
                     const int k = min(k0 + bk4 + e * RB4, K - 1);
                     const float *row = B + (uint32_t)(k * ldb);
                     if (!EDGE) {
-                        r.b4[e] = ld4(row + gn4);
+                        r.b4[e] = ld4(row + min(gn4, N - 4));
                     } else {
                         r.b4[e].x = row[min(gn4 + 0, N - 1)];
                         r.b4[e].y = row[min(gn4 + 1, N - 1)];
@@ -351,7 +355,9 @@ __global__ __launch_bounds__(kThreads) void k_gemm(GemmArgs g, SplitArgs sp, int
         }
         if (it < nk) compute(0);
     };
-    if (m0 + BM > M || n0 + BN > N)
+    const bool edge_m = AMODE == 0 && m0 + BM > M && (M & 3) != 0;  // row-major A clamps rows itself
+    const bool edge_n = BMODE == 0 && n0 + BN > N && (N & 3) != 0;  // im2col B masks per element
+    if (edge_m || edge_n)
         body(std::true_type{});
     else
         body(std::false_type{});
