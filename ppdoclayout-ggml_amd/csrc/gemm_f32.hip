@@ -84,6 +84,94 @@ struct Stage {
     uint32_t ok1;  // im2col: bit e set when element e is inside the image
 };
 
+// Epilogue of a wave's (32 TM) x (32 TN) accumulator tile whose top-left
+// output is (mw, nw): split-K partials, or bias / residual add / act and the
+// store in C's layout.  32x32 accumulator layout: lane owns column (lane & 31)
+// and rows 8*(r/4) + 4*(lane/32) + r%4 of register r.
+template <int TM, int TN, bool SPLIT>
+__device__ __forceinline__ void gemm_epilogue(const f32x16 (&acc)[TM][TN], const GemmArgs &g, const SplitArgs &sp,
+                                              int split, int bz, int mw, int nw, int lane) {
+    const int M = g.M, N = g.N, l32 = lane & 31;
+    if (SPLIT) {
+        float *__restrict__ P = sp.partials + ((int64_t)split * g.batch + bz) * M * N;
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+            const int n = nw + j * 32 + l32;
+            if (n < N) {
+#pragma unroll
+                for (int i = 0; i < TM; i++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++) {
+                        const int m = mw + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                        if (m < M) P[(int64_t)m * N + n] = acc[i][j][r];
+                    }
+            }
+        }
+        return;
+    }
+
+    const float *__restrict__ bias = g.bias;
+    const int act = g.act, add_mode = g.add_mode, bias_n = g.bias_n;
+    float *__restrict__ C = g.C + (int64_t)bz * g.sC;
+    const float *__restrict__ Ad = g.add ? g.add + (int64_t)bz * g.sC : nullptr;
+    auto epi = [&](float v, int m, int n, int64_t idx) {
+        if (bias) v += bias[bias_n ? n : m];
+        if (add_mode == 1) v += Ad[idx];
+        v = act_f(v, act);
+        if (add_mode == 2) v += Ad[idx];
+        return v;
+    };
+    if (!g.c_trans) {
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+            const int n = nw + j * 32 + l32;
+            if (n < N) {
+#pragma unroll
+                for (int i = 0; i < TM; i++) {
+#pragma unroll
+                    for (int r = 0; r < 16; r++) {
+                        const int m = mw + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                        if (m < M) {
+                            const int64_t idx = (int64_t)m * g.ldc + n;
+                            C[idx] = epi(acc[i][j][r], m, n, idx);
+                        }
+                    }
+                }
+            }
+        }
+    } else {
+        // C[n][m]: registers 4g..4g+3 hold 4 consecutive m of one n
+        const bool vec_ok = (g.ldc % 4 == 0) && ((((uintptr_t)C) & 15) == 0) &&
+                            (!Ad || ((((uintptr_t)Ad) & 15) == 0));
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+            const int n = nw + j * 32 + l32;
+            if (n < N) {
+#pragma unroll
+                for (int i = 0; i < TM; i++) {
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        const int mb = mw + i * 32 + 8 * q + 4 * (lane >> 5);
+                        const int64_t idx = (int64_t)n * g.ldc + mb;
+                        if (vec_ok && mb + 3 < M) {
+                            float4 v;
+                            v.x = epi(acc[i][j][4 * q + 0], mb + 0, n, idx + 0);
+                            v.y = epi(acc[i][j][4 * q + 1], mb + 1, n, idx + 1);
+                            v.z = epi(acc[i][j][4 * q + 2], mb + 2, n, idx + 2);
+                            v.w = epi(acc[i][j][4 * q + 3], mb + 3, n, idx + 3);
+                            *reinterpret_cast<float4 *>(C + idx) = v;
+                        } else {
+#pragma unroll
+                            for (int u = 0; u < 4; u++)
+                                if (mb + u < M) C[idx + u] = epi(acc[i][j][4 * q + u], mb + u, n, idx + u);
+                        }
+                    }
+                }
+            }
+        }
+    }
+}
+
 // AMODE 0: A k-major; AMODE 1: A row-major (K % 4 == 0, lda % 4 == 0).
 // BMODE 0: dense B; BMODE 1: implicit im2col B.
 template <int BM, int BN, int WGM, int AMODE, int BMODE, bool SPLIT>
@@ -362,86 +450,162 @@ __global__ __launch_bounds__(kThreads) void k_gemm(GemmArgs g, SplitArgs sp, int
     else
         body(std::false_type{});
 
-    // 32x32 accumulator layout: lane owns column (lane & 31) and rows
-    // 8*(r/4) + 4*(lane/32) + r%4 of register r
-    if (SPLIT) {
-        float *__restrict__ P = sp.partials + ((int64_t)split * g.batch + bz) * M * N;
-#pragma unroll
-        for (int j = 0; j < TN; j++) {
-            const int n = n0 + wn0 + j * 32 + l32;
-            if (n < N) {
-#pragma unroll
-                for (int i = 0; i < TM; i++)
-#pragma unroll
-                    for (int r = 0; r < 16; r++) {
-                        const int m = m0 + wm0 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                        if (m < M) P[(int64_t)m * N + n] = acc[i][j][r];
-                    }
-            }
-        }
-        return;
-    }
+    gemm_epilogue<TM, TN, SPLIT>(acc, g, sp, split, bz, m0 + wm0, n0 + wn0, lane);
+}
 
-    const float *__restrict__ bias = g.bias;
-    const int act = g.act, add_mode = g.add_mode, bias_n = g.bias_n;
-    float *__restrict__ C = g.C + (int64_t)bz * g.sC;
-    const float *__restrict__ Ad = g.add ? g.add + (int64_t)bz * g.sC : nullptr;
-    auto epi = [&](float v, int m, int n, int64_t idx) {
-        if (bias) v += bias[bias_n ? n : m];
-        if (add_mode == 1) v += Ad[idx];
-        v = act_f(v, act);
-        if (add_mode == 2) v += Ad[idx];
-        return v;
-    };
-    if (!g.c_trans) {
+// ---------------------------------------------------------------------------
+// Direct-to-LDS variant for dense k-major A and B (1x1 convs, F(4,3) planes)
+// whose M, N, lda, ldb are multiples of 4 with 16-byte aligned bases.  Each
+// wave moves its share of a k tile with global_load_lds_dwordx4 (16 bytes per
+// lane into m0 + 16 * lane): no staging registers, no LDS store instructions,
+// and the next tile's copy is in flight while the current one is consumed.
+// The LDS tile is [k][m] (resp. [k][n]) unpadded, 4 rows of 64 floats or 8
+// of 32 per wave instruction.
+//
+// The copy is issued through inline asm: the compiler's own LDS-DMA tracking
+// cannot tell the stages apart and would drain every copy before any LDS
+// read.  Ordering is explicit instead: s_waitcnt vmcnt for this wave's copies
+// of the tile, then the block barrier for everyone else's.
+//
+// Edges: rows past K and columns past M / N are clamped to valid addresses
+// (finite values that only reach discarded outputs); on the global last k
+// tile, A rows at or past K are zeroed in LDS before use.
+typedef __attribute__((address_space(3))) float lds_f32;
+__device__ __forceinline__ uint32_t lds_off(float *p) { return (uint32_t)(uintptr_t)(lds_f32 *)p; }
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"  // m0 is reserved: nothing else in these kernels uses it
+__device__ __forceinline__ void dma16(const float *g, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(__builtin_amdgcn_readfirstlane(lds))
+                 : "memory", "m0");
+}
+#pragma clang diagnostic pop
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((((N >> 4) & 3) << 14) | (0xF << 8) | (0x7 << 4) | (N & 0xF));
+}
+
+template <int BM, int BN, int WGM, bool SPLIT>
+__global__ __launch_bounds__(kThreads) void k_gemm_dma(GemmArgs g, SplitArgs sp, int tiles_m, int tiles_mn) {
+    constexpr int NS = 2;  // LDS stages: one tile computed while the next lands
+    constexpr int WGN = 4 / WGM, WM = BM / WGM, WN = BN / WGN, TM = WM / 32, TN = WN / 32;
+    constexpr int IA = kBK * BM / 4 / kThreads, IB = kBK * BN / 4 / kThreads;  // copies per wave per tile
+    constexpr int KH = kBK / 2, NP = KH / 2;
+    static_assert(IA >= 1 && IB >= 1 && TM >= 1 && TN >= 1, "bad tile");
+    __shared__ __attribute__((aligned(1024))) float As[NS][kBK * BM];
+    __shared__ __attribute__((aligned(1024))) float Bs[NS][kBK * BN];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int logical = xcd_remap(blockIdx.x, gridDim.x);
+    const int S = SPLIT ? sp.splits : 1;
+    const int split = SPLIT ? logical % S : 0;
+    const int tile_id = SPLIT ? logical / S : logical;
+    const int bz = tile_id / tiles_mn;
+    const int t = tile_id - bz * tiles_mn;
+    const int m0 = (t % tiles_m) * BM, n0 = (t / tiles_m) * BN;
+    const int M = g.M, N = g.N, K = g.K;
+    const int nk_total = (K + kBK - 1) / kBK;
+    const int kt0 = SPLIT ? split * sp.ktiles_per_split : 0;
+    const int kt1 = SPLIT ? min(nk_total, kt0 + sp.ktiles_per_split) : nk_total;
+    const int nk = kt1 - kt0;
+    const float *__restrict__ A = g.A + (int64_t)bz * g.sA;
+    const float *__restrict__ B = g.B + (int64_t)bz * g.sB;
+    const int lda = (int)g.lda, ldb = (int)g.ldb;
+
+    // this lane's chunk of each copy: tile row and clamped column
+    int ar[IA], ac[IA], br[IB], bc[IB];
 #pragma unroll
-        for (int j = 0; j < TN; j++) {
-            const int n = n0 + wn0 + j * 32 + l32;
-            if (n < N) {
-#pragma unroll
-                for (int i = 0; i < TM; i++) {
-#pragma unroll
-                    for (int r = 0; r < 16; r++) {
-                        const int m = m0 + wm0 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                        if (m < M) {
-                            const int64_t idx = (int64_t)m * g.ldc + n;
-                            C[idx] = epi(acc[i][j][r], m, n, idx);
-                        }
-                    }
-                }
-            }
-        }
-    } else {
-        // C[n][m]: registers 4g..4g+3 hold 4 consecutive m of one n
-        const bool vec_ok = (g.ldc % 4 == 0) && ((((uintptr_t)C) & 15) == 0) &&
-                            (!Ad || ((((uintptr_t)Ad) & 15) == 0));
-#pragma unroll
-        for (int j = 0; j < TN; j++) {
-            const int n = n0 + wn0 + j * 32 + l32;
-            if (n < N) {
-#pragma unroll
-                for (int i = 0; i < TM; i++) {
-#pragma unroll
-                    for (int q = 0; q < 4; q++) {
-                        const int mb = m0 + wm0 + i * 32 + 8 * q + 4 * (lane >> 5);
-                        const int64_t idx = (int64_t)n * g.ldc + mb;
-                        if (vec_ok && mb + 3 < M) {
-                            float4 v;
-                            v.x = epi(acc[i][j][4 * q + 0], mb + 0, n, idx + 0);
-                            v.y = epi(acc[i][j][4 * q + 1], mb + 1, n, idx + 1);
-                            v.z = epi(acc[i][j][4 * q + 2], mb + 2, n, idx + 2);
-                            v.w = epi(acc[i][j][4 * q + 3], mb + 3, n, idx + 3);
-                            *reinterpret_cast<float4 *>(C + idx) = v;
-                        } else {
-#pragma unroll
-                            for (int u = 0; u < 4; u++)
-                                if (mb + u < M) C[idx + u] = epi(acc[i][j][4 * q + u], mb + u, n, idx + u);
-                        }
-                    }
-                }
-            }
-        }
+    for (int e = 0; e < IA; e++) {
+        const int c = (wave * IA + e) * 64 + lane;
+        ar[e] = c / (BM / 4);
+        ac[e] = min(m0 + (c % (BM / 4)) * 4, M - 4);
     }
+#pragma unroll
+    for (int e = 0; e < IB; e++) {
+        const int c = (wave * IB + e) * 64 + lane;
+        br[e] = c / (BN / 4);
+        bc[e] = min(n0 + (c % (BN / 4)) * 4, N - 4);
+    }
+    auto issue = [&](int s, int kt) {
+        const int k0 = kt * kBK;
+#pragma unroll
+        for (int e = 0; e < IA; e++)
+            dma16(A + (uint32_t)(min(k0 + ar[e], K - 1) * lda + ac[e]), lds_off(&As[s][(wave * IA + e) * 256]));
+#pragma unroll
+        for (int e = 0; e < IB; e++)
+            dma16(B + (uint32_t)(min(k0 + br[e], K - 1) * ldb + bc[e]), lds_off(&Bs[s][(wave * IB + e) * 256]));
+    };
+
+    f32x16 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
+    const int wm0 = (wave % WGM) * WM, wn0 = (wave / WGM) * WN;
+    const int l32 = lane & 31, lk = (lane >> 5) * KH;
+
+    auto compute = [&](int s) {
+        float2 fa[NP][TM], fb[NP][TN];
+        auto rd = [&](int p) {
+#pragma unroll
+            for (int i = 0; i < TM; i++) {
+                fa[p][i].x = As[s][(lk + 2 * p) * BM + wm0 + i * 32 + l32];
+                fa[p][i].y = As[s][(lk + 2 * p + 1) * BM + wm0 + i * 32 + l32];
+            }
+#pragma unroll
+            for (int j = 0; j < TN; j++) {
+                fb[p][j].x = Bs[s][(lk + 2 * p) * BN + wn0 + j * 32 + l32];
+                fb[p][j].y = Bs[s][(lk + 2 * p + 1) * BN + wn0 + j * 32 + l32];
+            }
+        };
+        rd(0);
+        rd(1);
+        __builtin_amdgcn_sched_group_barrier(0x100, 2 * (TM + TN), 0);
+#pragma unroll
+        for (int p = 0; p < NP; p++) {
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int j = 0; j < TN; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[p][i].x, fb[p][j].x, acc[i][j], 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int j = 0; j < TN; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[p][i].y, fb[p][j].y, acc[i][j], 0, 0, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 2 * TM * TN, 0);
+            if (p + 2 < NP) {
+                rd(p + 2);
+                __builtin_amdgcn_sched_group_barrier(0x100, TM + TN, 0);
+            }
+        }
+    };
+
+    if (nk > 0) {
+        const int klast = kt1 - 1;
+        const int ktail = K - (nk_total - 1) * kBK;  // valid rows of the global last tile
+        issue(0, kt0);
+        for (int it = 0; it < nk; it += NS) {
+#pragma unroll
+            for (int u = 0; u < NS; u++) {
+                if (it + u < nk) {
+                    const int kt = kt0 + it + u;
+                    wait_vmcnt<(NS - 2) * (IA + IB)>();  // this wave's copies of tile kt have landed
+                    __syncthreads();                     // everyone's have; tile kt-1 is consumed
+                    if (kt == nk_total - 1 && ktail < kBK) {
+                        for (int i = tid; i < (kBK - ktail) * BM; i += kThreads) As[u][ktail * BM + i] = 0.0f;
+                        __syncthreads();
+                    }
+                    issue((u + 1) % NS, min(kt + 1, klast));
+                    compute(u);
+                }
+            }
+        }
+        wait_vmcnt<0>();  // no copy may still target this block's LDS when it exits
+    }
+    gemm_epilogue<TM, TN, SPLIT>(acc, g, sp, split, bz, m0 + wm0, n0 + wn0, lane);
 }
 
 // Split-K fix-up: the GEMM epilogue applied to sum_{s=0..S-1} P[s], s
@@ -648,6 +812,18 @@ int env_override(int *cfg, int *splits) {
     return 1;
 }
 
+// The direct-to-LDS kernel applies to dense k-major operands with 4-aligned
+// extents and 16-byte aligned bases (PPDL_GEMM_DMA=0 turns it off).
+bool dma_ok(const GemmArgs &g) {
+    static const bool off = [] {
+        const char *e = getenv("PPDL_GEMM_DMA");
+        return e && e[0] == '0';
+    }();
+    const auto a16 = [](const void *p) { return (((uintptr_t)p) & 15) == 0; };
+    return !off && !g.a_rowmajor && g.M >= 4 && g.N >= 4 && g.M % 4 == 0 && g.N % 4 == 0 && g.lda % 4 == 0 &&
+           g.ldb % 4 == 0 && g.sA % 4 == 0 && g.sB % 4 == 0 && a16(g.A) && a16(g.B);
+}
+
 template <int BM, int BN, int WGM, int AMODE, int BMODE>
 hipError_t launch(const GemmArgs &g, int S, const GemmWorkspace &ws, hipStream_t s) {
     const int tiles_m = (g.M + BM - 1) / BM, tiles_n = (g.N + BN - 1) / BN;
@@ -664,8 +840,12 @@ hipError_t launch(const GemmArgs &g, int S, const GemmWorkspace &ws, hipStream_t
         sp.splits = S;
         sp.ktiles_per_split = (nk + S - 1) / S;
         sp.partials = (float *)ws.base;
-        hipLaunchKernelGGL((k_gemm<BM, BN, WGM, AMODE, BMODE, true>), dim3((unsigned)total), dim3(kThreads), 0,
-                           s, g, sp, tiles_m, tiles_m * tiles_n);
+        if (AMODE == 0 && BMODE == 0 && dma_ok(g))
+            hipLaunchKernelGGL((k_gemm_dma<BM, BN, WGM, true>), dim3((unsigned)total), dim3(kThreads), 0, s, g, sp,
+                               tiles_m, tiles_m * tiles_n);
+        else
+            hipLaunchKernelGGL((k_gemm<BM, BN, WGM, AMODE, BMODE, true>), dim3((unsigned)total), dim3(kThreads), 0,
+                               s, g, sp, tiles_m, tiles_m * tiles_n);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
         const int64_t n = (int64_t)g.M * g.N * g.batch;
@@ -676,6 +856,9 @@ hipError_t launch(const GemmArgs &g, int S, const GemmWorkspace &ws, hipStream_t
         else
             hipLaunchKernelGGL(k_splitk_reduce<1>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
                                sp.partials, S, n, g);
+    } else if (AMODE == 0 && BMODE == 0 && dma_ok(g)) {
+        hipLaunchKernelGGL((k_gemm_dma<BM, BN, WGM, false>), dim3((unsigned)total), dim3(kThreads), 0, s, g, sp,
+                           tiles_m, tiles_m * tiles_n);
     } else {
         hipLaunchKernelGGL((k_gemm<BM, BN, WGM, AMODE, BMODE, false>), dim3((unsigned)total), dim3(kThreads), 0,
                            s, g, sp, tiles_m, tiles_m * tiles_n);
@@ -758,8 +941,12 @@ std::string gemm_kernel_name(const GemmArgs &g, int64_t ws_bytes, bool im2col) {
     int bm = kCfgs[p.cfg].bm, bn = kCfgs[p.cfg].bn, wgm = kCfgs[p.cfg].wgm;
     if (g.a_rowmajor && p.cfg != 5) bm = 64, bn = 64, wgm = 2;  // the two row-major-A shapes
     char buf[96];
-    snprintf(buf, sizeof(buf), "k_gemm<%d, %d, %d, %d, %d, %s>%s", bm, bn, wgm, g.a_rowmajor ? 1 : 0, im2col ? 1 : 0,
-             p.splits > 1 ? "true" : "false", p.splits > 1 ? "+k_splitk_reduce" : "");
+    if (!im2col && dma_ok(g))
+        snprintf(buf, sizeof(buf), "k_gemm_dma<%d, %d, %d, %s>%s", bm, bn, wgm, p.splits > 1 ? "true" : "false",
+                 p.splits > 1 ? "+k_splitk_reduce" : "");
+    else
+        snprintf(buf, sizeof(buf), "k_gemm<%d, %d, %d, %d, %d, %s>%s", bm, bn, wgm, g.a_rowmajor ? 1 : 0,
+                 im2col ? 1 : 0, p.splits > 1 ? "true" : "false", p.splits > 1 ? "+k_splitk_reduce" : "");
     return buf;
 }
 hipError_t gemm_im2col(const GemmArgs &g, const GemmWorkspace &ws, hipStream_t s) { return dispatch<1>(g, ws, s); }
