@@ -28,7 +28,7 @@ __global__ __launch_bounds__(256) void k_msdeform(const float *__restrict__ val,
                                                   const float *__restrict__ off,
                                                   const float *__restrict__ awr,
                                                   const float *__restrict__ ref,
-                                                  float *__restrict__ out, int nq) {
+                                                  float *__restrict__ out, int nq, int ldv) {
     const int q = blockIdx.x;
     if (q >= nq) return;
     const int h = threadIdx.x >> 5, c = threadIdx.x & 31;
@@ -75,7 +75,7 @@ __global__ __launch_bounds__(256) void k_msdeform(const float *__restrict__ val,
                 const int xx = x0 + (k & 1), yy = y0 + (k >> 1);
                 if (xx < 0 || xx >= W || yy < 0 || yy >= H || cw[k] == 0.0f) continue;
                 const float ww = wt * cw[k];
-                acc = fmaf(ww, vh[(int64_t)(st + yy * W + xx) * kDM], acc);
+                acc = fmaf(ww, vh[(int64_t)(st + yy * W + xx) * ldv], acc);
             }
         }
     }
@@ -296,9 +296,9 @@ __global__ __launch_bounds__(kTopkThreads) void k_topk(const float *__restrict__
 
 }  // namespace
 
-hipError_t msdeform(const float *val, const float *off, const float *awr, const float *ref,
+hipError_t msdeform(const float *val, int ldv, const float *off, const float *awr, const float *ref,
                     float *out, int nq, hipStream_t s) {
-    hipLaunchKernelGGL(k_msdeform, dim3(nq), dim3(256), 0, s, val, off, awr, ref, out, nq);
+    hipLaunchKernelGGL(k_msdeform, dim3(nq), dim3(256), 0, s, val, off, awr, ref, out, nq, ldv);
     return hipGetLastError();
 }
 

@@ -50,6 +50,9 @@ struct Node {
     std::string name;
     int kernels;  // device kernels this node launches
     std::function<int(hipStream_t)> run;
+    int lane = 0;  // stream the node runs on (0 = the graph's main stream)
+    int kind = 0;  // 0 kernels, 1 fork (lane waits for main), 2 join (main waits for lane)
+    int ev = -1;   // fork / join: index of its event
     int cls = 0;         // 0 other, 1 conv GEMM, 2 linear GEMM
     double flops = 0.0;  // algorithmic GEMM FLOP per run
     double bytes = 0.0;  // compulsory GEMM operand bytes per run
@@ -99,6 +102,9 @@ class Net {
     ~Net() {
         if (exec_) (void)hipGraphExecDestroy(exec_);
         if (graph_) (void)hipGraphDestroy(graph_);
+        for (hipEvent_t e : events_) (void)hipEventDestroy(e);
+        for (int l = 1; l < kLanes; l++)
+            if (lanes_[l]) (void)hipStreamDestroy(lanes_[l]);
         if (stream_) (void)hipStreamDestroy(stream_);
         for (void *p : allocs_) (void)hipFree(p);
     }
@@ -163,7 +169,38 @@ class Net {
     // ---- node emission ----
     void node(const std::string &name, int kernels, std::function<int(hipStream_t)> fn) {
         nodes_.push_back({name, kernels, std::move(fn)});
+        nodes_.back().lane = lane_;
     }
+    // Independent branches: fork(l) makes lane l wait for everything emitted
+    // so far on the main lane and directs the following nodes to lane l;
+    // main() directs them back without a dependency; join(l) makes the main
+    // lane wait for everything lane l has been given.  Each lane has its own
+    // scratch (F(4,3) planes, split-K workspace), so branches never share it.
+    void fork(int l) {
+        if (!multi_lane_) return;
+        sync_node("fork", 1, l);
+        lane_ = l;
+    }
+    void main_lane() { lane_ = 0; }
+    void join(int l) {
+        if (!multi_lane_) return;
+        sync_node("join", 2, l);
+        lane_ = 0;
+    }
+    void sync_node(const char *nm, int kind, int l) {
+        hipEvent_t e = nullptr;
+        if (hipEventCreateWithFlags(&e, hipEventDisableTiming) != hipSuccess) {
+            if (bad_node_.empty()) bad_node_ = nm;
+            return;
+        }
+        events_.push_back(e);
+        Node n{std::string(nm) + std::to_string(l), 0, nullptr};
+        n.lane = l;
+        n.kind = kind;
+        n.ev = (int)events_.size() - 1;
+        nodes_.push_back(std::move(n));
+    }
+    int launch_all();  // every node, on its lane, in list order
     // GEMM bookkeeping of the node just emitted (for ppdl_profile_nodes)
     void gemm_meta(int cls, const GemmArgs &g, int64_t ws_bytes, bool im2col) {
         Node &n = nodes_.back();
@@ -183,11 +220,12 @@ class Net {
             if (bad_node_.empty()) bad_node_ = name;
             return;
         }
-        ws_need_ = std::max(ws_need_, wsb);
+        Scratch *sc = &sc_[lane_];
+        sc->ws_need = std::max(sc->ws_need, wsb);
         const int kernels = (op == PPDL_OP_WG4_INPUT_PAD || op == PPDL_OP_WG4_OUTPUT) ? 1 : (wsb > 0 ? 2 : 1);
-        node(name, kernels, [this, pv, dst, src, wsb](hipStream_t s) {
+        node(name, kernels, [sc, pv, dst, src, wsb](hipStream_t s) {
             std::vector<ppdl_tview> sv = src;
-            if (wsb > 0) sv.push_back(view(ws_, {(ws_bytes_ + 3) / 4}));
+            if (wsb > 0) sv.push_back(view(sc->ws, {(sc->ws_bytes + 3) / 4}));
             return ppdl_hip_run(pv.data(), &dst, sv.data(), (int)sv.size(), s);
         });
         GemmArgs g;
@@ -196,9 +234,10 @@ class Net {
     }
     void gemm(const std::string &name, GemmArgs g) {
         const int64_t wsb = gemm_ws_bytes_for(g, false);
-        ws_need_ = std::max(ws_need_, wsb);
-        node(name, wsb > 0 ? 2 : 1, [this, g, wsb](hipStream_t s) {
-            GemmWorkspace ws{wsb > 0 ? ws_ : nullptr, wsb > 0 ? ws_bytes_ : 0};
+        Scratch *sc = &sc_[lane_];
+        sc->ws_need = std::max(sc->ws_need, wsb);
+        node(name, wsb > 0 ? 2 : 1, [sc, g, wsb](hipStream_t s) {
+            GemmWorkspace ws{wsb > 0 ? sc->ws : nullptr, wsb > 0 ? sc->ws_bytes : 0};
             return gemm_dense(g, ws, s) == hipSuccess ? 0 : 3;
         });
         gemm_meta(2, g, wsb, false);
@@ -221,12 +260,25 @@ class Net {
     std::map<std::string, float *> w_;
     std::map<std::string, std::vector<int64_t>> ne_;
     std::vector<Node> nodes_;
-    std::string missing_, bad_node_;
+    std::string missing_, bad_node_, failed_;
     bool oom_ = false, want_dumps_ = false;
-    int64_t ws_need_ = 0, ws_bytes_ = 0;
-    void *ws_ = nullptr;
-    float *wg_dt_ = nullptr, *wg_yt_ = nullptr;  // shared F(4,3) intermediates
-    int64_t wg_need_ = 0;
+    // per-lane scratch shared by that lane's nodes (they run in order)
+    struct Scratch {
+        int64_t ws_need = 0, ws_bytes = 0;  // split-K / top-k workspace
+        void *ws = nullptr;
+        int64_t wg_need = 0;  // F(4,3) dt / yt planes
+        float *dt = nullptr, *yt = nullptr;
+    };
+    static constexpr int kLanes = 3;
+    Scratch sc_[kLanes];
+    int lane_ = 0;
+    // Branches on separate streams (PPDL_GRAPH_LANES=1).  Off by default:
+    // measured on MI355X / ROCm 7, the captured graph with two side branches
+    // replays ~0.14 ms slower than the same nodes on one stream, more than
+    // the ~0.2 ms of overlappable work it gains.
+    bool multi_lane_ = false;
+    hipStream_t lanes_[kLanes] = {};  // lanes_[0] is stream_
+    std::vector<hipEvent_t> events_;
     hipStream_t stream_ = nullptr;
     hipGraph_t graph_ = nullptr;
     hipGraphExec_t exec_ = nullptr;
@@ -298,6 +350,42 @@ bool Net::load(const std::string &path, std::string *err) {
         w_[a + ".qk.bias"] = upload(b);
         ne_[a + ".qk.weight"] = {in, 2 * out};
     }
+    // the six decoder layers' value projections read the same encoder
+    // tokens: one [256][6*256] weight, so they run as one GEMM
+    {
+        std::vector<float> wt, b;
+        int64_t in = 0, out = 0;
+        bool all = true;
+        for (int i = 0; i < 6 && all; i++) {
+            const std::string a = "dec" + std::to_string(i) + ".ca.vp";
+            if (!g.index.count(a + ".weight") || !g.index.count(a + ".bias")) {
+                all = false;
+                break;
+            }
+            const auto &tw = g.tensors[g.index[a + ".weight"]];
+            if (i == 0) {
+                in = tw.ne[0];
+                out = tw.ne[1];
+                wt.assign((size_t)(in * 6 * out), 0.0f);
+                b.assign((size_t)(6 * out), 0.0f);
+            } else if (tw.ne[0] != in || tw.ne[1] != out) {
+                all = false;
+                break;
+            }
+            std::vector<float> h((size_t)(in * out)), hb((size_t)out);
+            if (!gguf_read_f32(g, tw, h.data(), err) || !gguf_read_f32(g, g.tensors[g.index[a + ".bias"]], hb.data(), err))
+                return false;
+            for (int64_t o = 0; o < out; o++) {
+                for (int64_t k = 0; k < in; k++) wt[(size_t)(k * 6 * out + i * out + o)] = h[(size_t)(o * in + k)];
+                b[(size_t)(i * out + o)] = hb[(size_t)o];
+            }
+        }
+        if (all && out > 0) {
+            w_["dec.ca.vp.wt"] = upload(wt);
+            w_["dec.ca.vp.bias"] = upload(b);
+            ne_["dec.ca.vp.weight"] = {in, 6 * out};
+        }
+    }
     if (oom_) {
         *err = "device allocation failed";
         return false;
@@ -331,7 +419,8 @@ Img Net::conv(const Img &x, const std::string &name, int s, int p, int act, floa
     } else if (K == 3 && s == 1 && p == 1 && pad_end == 0 && add_mode == 0) {
         // Winograd F(4,3): pad fused into op 15, madd (op 12), output + bias + act (op 11) (:425-463)
         const int TW = (OW + 3) / 4, TH = (OH + 3) / 4, T = TW * TH;
-        wg_need_ = std::max(wg_need_, (int64_t)36 * std::max(x.C, OC) * T);
+        Scratch *sc = &sc_[lane_];
+        sc->wg_need = std::max(sc->wg_need, (int64_t)36 * std::max(x.C, OC) * T);
         // The 36-plane intermediates dt / yt are shared by every Winograd
         // conv and allocated once the largest is known, so the launches
         // read their address at run time.  The workspace query only reads
@@ -344,15 +433,15 @@ Img Net::conv(const Img &x, const std::string &name, int s, int p, int act, floa
         const ppdl_tview qs[2] = {view(kShapeOnly, {T, x.C, 36}), view(wg4, {OC, x.C, 36})};
         const int64_t wsb = ppdl_hip_workspace_bytes(p_md.data(), &qd, qs, 2);
         if (wsb < 0 && bad_node_.empty()) bad_node_ = name;
-        ws_need_ = std::max(ws_need_, wsb);
+        sc->ws_need = std::max(sc->ws_need, wsb);
         node(name + ".wg_in", 1, [=](hipStream_t st) {
-            ppdl_tview d = view(wg_dt_, {T, xi.C, 36}), sx = view(xi);
+            ppdl_tview d = view(sc->dt, {T, xi.C, 36}), sx = view(xi);
             return ppdl_hip_run(p_in.data(), &d, &sx, 1, st);
         });
         node(name + ".wg_madd", wsb > 0 ? 2 : 1, [=](hipStream_t st) {
-            ppdl_tview d = view(wg_yt_, {T, OC, 36});
-            std::vector<ppdl_tview> sv = {view(wg_dt_, {T, xi.C, 36}), view(wg4, {OC, xi.C, 36})};
-            if (wsb > 0) sv.push_back(view(ws_, {(ws_bytes_ + 3) / 4}));
+            ppdl_tview d = view(sc->yt, {T, OC, 36});
+            std::vector<ppdl_tview> sv = {view(sc->dt, {T, xi.C, 36}), view(wg4, {OC, xi.C, 36})};
+            if (wsb > 0) sv.push_back(view(sc->ws, {(sc->ws_bytes + 3) / 4}));
             return ppdl_hip_run(p_md.data(), &d, sv.data(), (int)sv.size(), st);
         });
         {
@@ -362,7 +451,7 @@ Img Net::conv(const Img &x, const std::string &name, int s, int p, int act, floa
         }
         node(name + ".wg_out", 1, [=](hipStream_t st) {
             ppdl_tview d = view(y);
-            ppdl_tview sv[2] = {view(wg_yt_, {T, OC, 36}), view(b, {OC})};
+            ppdl_tview sv[2] = {view(sc->yt, {T, OC, 36}), view(b, {OC})};
             return ppdl_hip_run(p_out.data(), &d, sv, 2, st);
         });
     } else {
@@ -466,10 +555,14 @@ Img Net::csp(const Img &x, const std::string &pfx, float *out) {
 // The full graph (builder::build, src/ppdoclayout.cpp:733-882).
 bool Net::build(bool dumps, std::string *err) {
     want_dumps_ = dumps;
-    if (hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking) != hipSuccess) {
-        *err = "hipStreamCreate failed";
-        return false;
+    for (int l = 0; l < kLanes; l++) {
+        if (hipStreamCreateWithFlags(&lanes_[l], hipStreamNonBlocking) != hipSuccess) {
+            *err = "hipStreamCreate failed";
+            return false;
+        }
     }
+    stream_ = lanes_[0];  // the main lane; destroyed as stream_
+    if (const char *e = getenv("PPDL_GRAPH_LANES")) multi_lane_ = e[0] == '1';
     image_ = alloc(3LL * IMG * IMG);
     pos_ = alloc(625LL * kDM);
     valid_ = alloc(NTOK);
@@ -546,7 +639,9 @@ bool Net::build(bool dumps, std::string *err) {
     Img n32 = csp(catp32, "pan1", nullptr);
     dump("n32", n32);
 
-    // mask feature head (:711-724)
+    // mask feature head (:711-724), on lane 1: only the encoder masks (after
+    // the top-300 selection) and the final masks read it
+    fork(1);
     Img h0 = conv(f8, "mh0.0", 1, 1, kActSilu);  // 100, 64
     Img h1 = conv(n16, "mh1.0", 1, 1, kActSilu);
     Img m1{alloc(64LL * 10000), 64, 100, 100};
@@ -564,6 +659,7 @@ bool Net::build(bool dumps, std::string *err) {
     Img mb = conv(mu, "mout.base", 1, 1, kActSilu);
     Img mask_feat = conv(mb, "mout.conv", 1, 0, kActNone);  // 200, 32
     dump("mask_feat", mask_feat);
+    main_lane();
 
     // ---- decoder inputs (:791-801): 1x1 projections written token-major
     // into one (13125, 256) source, level after level
@@ -591,6 +687,15 @@ bool Net::build(bool dumps, std::string *err) {
         }
     }
     dump("source", source.d, {kDM, NTOK});
+    // value projections of all six decoder layers at once (layer i: columns
+    // 256i..256i+255), on lane 2 until the first deformable attention
+    const bool vp_cat = w_.count("dec.ca.vp.wt") != 0;
+    Seq vcat{};
+    if (vp_cat) {
+        fork(2);
+        vcat = lin(source, "dec.ca.vp", kActNone);
+        main_lane();
+    }
     Seq memory{alloc((int64_t)NTOK * kDM), NTOK, kDM, kDM};
     node("memory", 1, [=](hipStream_t st) { return ok(mul_rows(source.d, valid_, memory.d, NTOK, kDM, st)); });
     Seq om = ln(lin(memory, "enc_out.l", kActNone), nullptr, "enc_out.ln");
@@ -621,6 +726,7 @@ bool Net::build(bool dumps, std::string *err) {
     Seq outq0 = ln(target, nullptr, "dec_norm");
     Seq mq0 = mlp3(outq0, "mq");
     float *encm = alloc((int64_t)NQ * NPIX);
+    join(1);
     masks_of(mq0, encm, "enc_masks");
     dump("enc_masks", encm, {NPIX, NQ});
     refu_ = alloc((int64_t)NQ * 4);
@@ -646,12 +752,20 @@ bool Net::build(bool dumps, std::string *err) {
         Seq z{alloc((int64_t)NQ * kDM), NQ, kDM, kDM};
         const Seq x1 = xq;
         node(dp + ".z", 1, [=](hipStream_t st) { return ok(add(x1.d, qpos.d, z.d, (int64_t)NQ * kDM, st)); });
-        Seq value = lin(source, dp + ".ca.vp", kActNone);
+        ppdl_tview vval;
+        if (vp_cat && i == 0) join(2);
+        if (vp_cat) {
+            vval = view(vcat.d + (int64_t)i * kDM, {kDM, NTOK});  // row stride 6*256
+            vval.nb[1] = (int64_t)vcat.ld * 4;
+            vval.nb[2] = vval.nb[3] = vval.nb[1] * NTOK;
+        } else {
+            vval = view(lin(source, dp + ".ca.vp", kActNone).d, {kDM, NTOK});
+        }
         Seq offs = lin(z, dp + ".ca.so", kActNone);
         Seq aw = lin(z, dp + ".ca.aw", kActNone);
         Seq ca{alloc((int64_t)NQ * kDM), NQ, kDM, kDM};
         tagged(dp + ".msdeform", PPDL_OP_MSDEF, 0, 0, view(ca.d, {kDM, NQ}),
-               {view(value.d, {kDM, NTOK}), view(offs.d, {192, NQ}), view(aw.d, {96, NQ}), view(ref.d, {4, NQ})});
+               {vval, view(offs.d, {192, NQ}), view(aw.d, {96, NQ}), view(ref.d, {4, NQ})});
         Seq cao = lin(ca, dp + ".ca.op", kActNone, nullptr, xq.d, 2);  // x + ca
         xq = ln(cao, nullptr, dp + ".ln2");
         Seq ff = lin(lin(xq, dp + ".fc1", kActRelu), dp + ".fc2", kActNone, nullptr, xq.d, 2);
@@ -681,10 +795,13 @@ bool Net::build(bool dumps, std::string *err) {
         *err = "node rejected by the op contract: " + bad_node_;
         return false;
     }
-    wg_dt_ = alloc(wg_need_);
-    wg_yt_ = alloc(wg_need_);
-    ws_bytes_ = (ws_need_ + 255) / 256 * 256;
-    ws_ = ws_bytes_ ? alloc(ws_bytes_ / 4) : nullptr;
+    if (lane_ != 0 && bad_node_.empty()) bad_node_ = "unjoined lane";
+    for (Scratch &sc : sc_) {
+        sc.dt = sc.wg_need ? alloc(sc.wg_need) : nullptr;
+        sc.yt = sc.wg_need ? alloc(sc.wg_need) : nullptr;
+        sc.ws_bytes = (sc.ws_need + 255) / 256 * 256;
+        sc.ws = sc.ws_bytes ? alloc(sc.ws_bytes / 4) : nullptr;
+    }
     if (oom_) {
         *err = "device allocation failed while building the graph";
         return false;
@@ -735,12 +852,9 @@ bool Net::capture(std::string *err) {
         *err = "image upload failed";
         return false;
     }
-    for (auto &n : nodes_) {
-        const int rc = n.run(stream_);
-        if (rc != 0) {
-            *err = "node " + n.name + " failed (" + std::to_string(rc) + ")";
-            return false;
-        }
+    if (const int rc = launch_all()) {
+        *err = "eager pass failed at node " + failed_ + " (" + std::to_string(rc) + ")";
+        return false;
     }
     if (hipStreamSynchronize(stream_) != hipSuccess) {
         *err = "eager pass failed";
@@ -750,9 +864,7 @@ bool Net::capture(std::string *err) {
         *err = "hipStreamBeginCapture failed";
         return false;
     }
-    int rc = 0;
-    for (auto &n : nodes_)
-        if (!rc) rc = n.run(stream_);
+    const int rc = launch_all();
     hipGraph_t g = nullptr;
     const hipError_t e = hipStreamEndCapture(stream_, &g);
     if (rc || e != hipSuccess || !g) {
@@ -766,6 +878,29 @@ bool Net::capture(std::string *err) {
         return false;
     }
     return true;
+}
+
+int Net::launch_all() {
+    for (auto &n : nodes_) {
+        int rc = 0;
+        if (n.kind == 1)
+            rc = (hipEventRecord(events_[n.ev], stream_) == hipSuccess &&
+                  hipStreamWaitEvent(lanes_[n.lane], events_[n.ev], 0) == hipSuccess)
+                     ? 0
+                     : 3;
+        else if (n.kind == 2)
+            rc = (hipEventRecord(events_[n.ev], lanes_[n.lane]) == hipSuccess &&
+                  hipStreamWaitEvent(stream_, events_[n.ev], 0) == hipSuccess)
+                     ? 0
+                     : 3;
+        else
+            rc = n.run(lanes_[n.lane]);
+        if (rc) {
+            failed_ = n.name;
+            return rc;
+        }
+    }
+    return 0;
 }
 
 bool Net::upload_image(const float *host) {
@@ -810,6 +945,7 @@ int Net::profile_nodes(int iters, ppdl_node_stat *out, int cap) {
     bool good = true;
     for (size_t i = 0; good && i < nodes_.size() && n < cap; i++) {
         Node &nd = nodes_[i];
+        if (nd.kind != 0) continue;
         for (int r = 0; good && r < 2; r++) good = nd.run(stream_) == 0;
         good = good && hipEventRecord(e0, stream_) == hipSuccess;
         for (int r = 0; good && r < iters; r++) good = nd.run(stream_) == 0;

@@ -111,7 +111,8 @@ hipError_t im2col_ggml(const float *x, float *dst, int64_t IW, int64_t IH, int64
                        hipStream_t s);
 
 // ---- decoder ops ----
-hipError_t msdeform(const float *val, const float *off, const float *awr, const float *ref,
+// val: 13125 token rows of 256 channels, row stride ldv (>= 256) floats
+hipError_t msdeform(const float *val, int ldv, const float *off, const float *awr, const float *ref,
                     float *out, int nq, hipStream_t s);
 hipError_t mask_box(const float *ml, float *out, int nq, hipStream_t s);
 // ws (optional, >= 8 * ntok bytes): per-token keys, computed grid-wide first

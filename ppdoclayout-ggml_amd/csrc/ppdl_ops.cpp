@@ -62,6 +62,16 @@ int ws_index(const int32_t *p) {
     }
 }
 
+// F32 rows: unit element stride, any row stride >= the row (a multiple of 4
+// bytes, below 2^31 elements), a single plane
+bool rows_f32(const ppdl_tview *t) {
+    if (!t || !t->data || t->type != PPDL_TYPE_F32 || t->nb[0] != 4) return false;
+    for (int i = 0; i < 4; i++)
+        if (t->ne[i] < 1) return false;
+    if (t->nb[1] < t->ne[0] * 4 || t->nb[1] % 4 != 0 || t->nb[1] / 4 > kMaxI32) return false;
+    return t->ne[2] == 1 && t->ne[3] == 1;
+}
+
 bool ws_valid(const ppdl_tview *t) {
     if (!t->data || (t->type != PPDL_TYPE_F32 && t->type != PPDL_TYPE_I32) || t->nb[0] != 4) return false;
     for (int i = 1; i < 4; i++)
@@ -170,7 +180,9 @@ int check_op(const int32_t *p, const ppdl_tview *dst, const ppdl_tview *src, int
         }
         case PPDL_OP_MSDEF: {
             if (nsrc < 4 || !contig_f32(dst)) return PPDL_EINVAL;
-            for (int i = 0; i < 4; i++)
+            // the value map may be a row-strided view (one slice of a wider projection)
+            if (!rows_f32(&src[0])) return PPDL_EINVAL;
+            for (int i = 1; i < 4; i++)
                 if (!contig_f32(&src[i])) return PPDL_EINVAL;
             const int64_t NQ = dst->ne[1];
             if (!shape_is(dst, kDM, NQ, 1, 1) || !shape_is(&src[0], kDM, kNTOK, 1, 1) ||
@@ -347,7 +359,7 @@ extern "C" PPDL_HIP_API int ppdl_hip_run(const int32_t op_params[16], const ppdl
                                         p[14], s));
         }
         case PPDL_OP_MSDEF:
-            return status_of(msdeform((const float *)src[0].data, (const float *)src[1].data,
+            return status_of(msdeform((const float *)src[0].data, (int)(src[0].nb[1] / 4), (const float *)src[1].data,
                                       (const float *)src[2].data, (const float *)src[3].data,
                                       (float *)dst->data, (int)dst->ne[1], s));
         case PPDL_OP_MASKBOX:

@@ -163,3 +163,21 @@ def test_misaligned_workspace_rejected(hip):
     v = lambda ne, p=FAKE: hip.raw_view(p, ne)  # noqa: E731
     srcs = [v([25, 25, 64]), v([32, 64, 1]), v([32]), v([1024], FAKE + 4)]
     assert hip.run(hip.OP_CONV1X1_BA, v([25, 25, 32]), srcs, 0, stream=0) == hip.EINVAL
+
+
+# ---------------------------------------------------------------- CLI (no GPU work)
+CLI = os.path.join(ROOT, "ppdoclayout-ggml_amd", "lib", "ppdoclayout")
+
+
+@pytest.mark.skipif(not os.path.exists(CLI), reason="CLI not built (make -C ppdoclayout-ggml_amd)")
+def test_cli_argument_handling(tmp_path):
+    import subprocess
+
+    r = subprocess.run([CLI], capture_output=True, text=True)
+    assert r.returncode == 1 and "usage:" in r.stderr
+    r = subprocess.run([CLI, "-i", "x.bin", "--bogus", "1"], capture_output=True, text=True)
+    assert r.returncode == 1 and "unknown arg" in r.stderr
+    r = subprocess.run([CLI, "-i", "x.bin", "--backend", "cpu"], capture_output=True, text=True)
+    assert r.returncode == 1 and "not available" in r.stderr
+    r = subprocess.run([CLI, "-i"], capture_output=True, text=True)
+    assert r.returncode == 1 and "missing value" in r.stderr

@@ -195,3 +195,31 @@ def test_dump_raw_files(gpu, tmp_path):
     lg = np.fromfile(pfx + "logits.bin", np.float32).reshape(300, 25)
     assert np.array_equal(lg, raw["logits"])
     assert os.path.getsize(pfx + "sel.bin") == 300 * 4
+
+
+def test_cli_matches_api(gpu, model, image, tmp_path):
+    """lib/ppdoclayout (the reference CLI's flags and files) on the same model
+    and page: out0/out2 equal the API's result, out1 holds the count; batch
+    mode writes the same files per manifest line."""
+    import subprocess
+
+    cli = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "ppdoclayout-ggml_amd", "lib",
+                       "ppdoclayout")
+    _, _, _, dets, masks = gpu
+    inp = tmp_path / "page.bin"
+    image.astype(np.float32).tofile(inp)
+    out = tmp_path / "single"
+    r = subprocess.run([cli, "-m", model[0], "-i", str(inp), "--ori-h", "1000", "--ori-w", "700", "-o", str(out),
+                        "--bench", "2"], capture_output=True, text=True, timeout=240)
+    say(r.stdout.strip(), r.stderr.strip().splitlines()[-1:])
+    assert r.returncode == 0, r.stderr
+    assert "bench_ms mean=" in r.stdout
+    assert np.array_equal(np.fromfile(out / "out0.bin", np.float32).reshape(300, 7), dets)
+    assert np.fromfile(out / "out1.bin", np.int32).tolist() == [300]
+    assert np.array_equal(np.fromfile(out / "out2.bin", np.int32).reshape(300, 200, 200), masks)
+    man = tmp_path / "manifest.txt"
+    man.write_text("%s|%s|1000|700\n%s|%s|1000|700\n" % (inp, tmp_path / "b0", inp, tmp_path / "b1"))
+    r = subprocess.run([cli, "-m", model[0], "--batch", str(man)], capture_output=True, text=True, timeout=240)
+    assert r.returncode == 0, r.stderr
+    for d in ("b0", "b1"):
+        assert np.array_equal(np.fromfile(tmp_path / d / "out0.bin", np.float32).reshape(300, 7), dets)

@@ -369,6 +369,30 @@ def hip_msdeform(hip, val, off, awr, ref):
     return host(out)
 
 
+def test_msdeform_row_strided_value(hip, orc):
+    """The value map may be a row-strided slice of a wider projection (the
+    runtime's six decoder layers share one 13125 x 1536 projection): same
+    result, bit for bit, as the contiguous map."""
+    val, off, awr, ref = msdef_config4(np.random.default_rng(SEED + 44))
+    wide = torch.full((val.shape[0], 1536), float("nan"), device="cuda")
+    wide[:, 512:768] = dev(val)
+    v = hip.TView()
+    v.data = wide.data_ptr() + 512 * 4
+    for i, (n, b) in enumerate(zip((256, val.shape[0], 1, 1), (4, 1536 * 4, 1536 * 4 * val.shape[0],
+                                                                    1536 * 4 * val.shape[0]))):
+        v.ne[i], v.nb[i] = n, b
+    v.type = hip.TYPE_F32
+    out = torch.empty((ref.shape[0], 256), device="cuda")
+    hip.run_checked(hip.OP_MSDEF, out, [v, dev(off), dev(awr), dev(ref)])
+    assert np.array_equal(host(out), hip_msdeform(hip, val, off, awr, ref))
+    bad = hip.TView()
+    bad.data, bad.type = v.data, v.type
+    for i, (n, b) in enumerate(zip((256, val.shape[0], 1, 1), (4, 255 * 4, 255 * 4 * val.shape[0],
+                                                                   255 * 4 * val.shape[0]))):
+        bad.ne[i], bad.nb[i] = n, b
+    assert hip.run(hip.OP_MSDEF, out, [bad, dev(off), dev(awr), dev(ref)]) == hip.EINVAL  # rows overlap
+
+
 def test_msdeform_config4(hip, orc):
     say("msdeform 300q x 8h x 3lvl x 4pt (config 4)")
     val, off, awr, ref = msdef_config4(np.random.default_rng(SEED + 4))
