@@ -51,7 +51,13 @@ __global__ __launch_bounds__(256) void k_msdeform(const float *__restrict__ val,
 
     const float *o = off + (int64_t)q * 192 + h * 24;
     const float *vh = val + h * kHD + c;
-    float acc = 0.0f;
+    // Corner tokens and weights first, the 48 gathers next (all issued
+    // together), the accumulation last in the reference's l -> p -> corner
+    // order.  A corner outside the map or with zero bilinear weight reads
+    // token 0 with weight 0: fmaf(0, v, acc) == acc, as if it were skipped.
+    constexpr int kS = 3 * 4 * 4;
+    float wv[kS];
+    int tok[kS];
 #pragma unroll
     for (int l = 0; l < 3; l++) {
         const int W = kLvlW[l], H = kLvlW[l], st = kLvlStart[l];
@@ -73,12 +79,19 @@ __global__ __launch_bounds__(256) void k_msdeform(const float *__restrict__ val,
 #pragma unroll
             for (int k = 0; k < 4; k++) {
                 const int xx = x0 + (k & 1), yy = y0 + (k >> 1);
-                if (xx < 0 || xx >= W || yy < 0 || yy >= H || cw[k] == 0.0f) continue;
-                const float ww = wt * cw[k];
-                acc = fmaf(ww, vh[(int64_t)(st + yy * W + xx) * ldv], acc);
+                const bool in = xx >= 0 && xx < W && yy >= 0 && yy < H && cw[k] != 0.0f;
+                const int i = (l * 4 + p) * 4 + k;
+                wv[i] = in ? wt * cw[k] : 0.0f;
+                tok[i] = in ? st + yy * W + xx : 0;
             }
         }
     }
+    float v[kS];
+#pragma unroll
+    for (int i = 0; i < kS; i++) v[i] = vh[(int64_t)tok[i] * ldv];
+    float acc = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kS; i++) acc = fmaf(wv[i], v[i], acc);
     out[(int64_t)q * kDM + h * kHD + c] = acc;
 }
 

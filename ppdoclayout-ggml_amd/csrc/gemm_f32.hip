@@ -231,6 +231,9 @@ __global__ __launch_bounds__(kThreads) void k_gemm(GemmArgs g, SplitArgs sp, int
     }
     // operand extents per batch plane fit in int32 (checked on the host)
     const int plane = g.IH * g.IW;
+    // last float4 start of a B row: N - 4, or the padded width - 4 when B's
+    // rows have room for whole float4s past N (columns nobody stores)
+    const int nclamp = (g.n_vec > 0 ? g.n_vec : N) - 4;
     const int lda = (int)g.lda, ldb = (int)g.ldb;
 
     f32x16 acc[TM][TN];
@@ -332,7 +335,7 @@ __global__ __launch_bounds__(kThreads) void k_gemm(GemmArgs g, SplitArgs sp, int
                     const int k = min(k0 + bk4 + e * RB4, K - 1);
                     const float *row = B + (uint32_t)(k * ldb);
                     if (!EDGE) {
-                        r.b4[e] = ld4(row + min(gn4, N - 4));
+                        r.b4[e] = ld4(row + min(gn4, nclamp));
                     } else {
                         r.b4[e].x = row[min(gn4 + 0, N - 1)];
                         r.b4[e].y = row[min(gn4 + 1, N - 1)];
@@ -444,7 +447,7 @@ __global__ __launch_bounds__(kThreads) void k_gemm(GemmArgs g, SplitArgs sp, int
         if (it < nk) compute(0);
     };
     const bool edge_m = AMODE == 0 && m0 + BM > M && (M & 3) != 0;  // row-major A clamps rows itself
-    const bool edge_n = BMODE == 0 && n0 + BN > N && (N & 3) != 0;  // im2col B masks per element
+    const bool edge_n = BMODE == 0 && n0 + BN > N && g.n_vec == 0;  // im2col B masks per element
     if (edge_m || edge_n)
         body(std::true_type{});
     else
@@ -467,8 +470,8 @@ __global__ __launch_bounds__(kThreads) void k_gemm(GemmArgs g, SplitArgs sp, int
 // read.  Ordering is explicit instead: s_waitcnt vmcnt for this wave's copies
 // of the tile, then the block barrier for everyone else's.
 //
-// Edges: rows past K and columns past M / N are clamped to valid addresses
-// (finite values that only reach discarded outputs); on the global last k
+// Edges: rows past K and columns past M / n_vec are clamped to valid
+// addresses (values that only reach discarded outputs); on the global last k
 // tile, A rows at or past K are zeroed in LDS before use.
 typedef __attribute__((address_space(3))) float lds_f32;
 __device__ __forceinline__ uint32_t lds_off(float *p) { return (uint32_t)(uintptr_t)(lds_f32 *)p; }
@@ -503,7 +506,7 @@ __global__ __launch_bounds__(kThreads) void k_gemm_dma(GemmArgs g, SplitArgs sp,
     const int bz = tile_id / tiles_mn;
     const int t = tile_id - bz * tiles_mn;
     const int m0 = (t % tiles_m) * BM, n0 = (t / tiles_m) * BN;
-    const int M = g.M, N = g.N, K = g.K;
+    const int M = g.M, K = g.K;
     const int nk_total = (K + kBK - 1) / kBK;
     const int kt0 = SPLIT ? split * sp.ktiles_per_split : 0;
     const int kt1 = SPLIT ? min(nk_total, kt0 + sp.ktiles_per_split) : nk_total;
@@ -524,7 +527,7 @@ __global__ __launch_bounds__(kThreads) void k_gemm_dma(GemmArgs g, SplitArgs sp,
     for (int e = 0; e < IB; e++) {
         const int c = (wave * IB + e) * 64 + lane;
         br[e] = c / (BN / 4);
-        bc[e] = min(n0 + (c % (BN / 4)) * 4, N - 4);
+        bc[e] = min(n0 + (c % (BN / 4)) * 4, g.n_vec - 4);
     }
     auto issue = [&](int s, int kt) {
         const int k0 = kt * kBK;
@@ -812,6 +815,13 @@ int env_override(int *cfg, int *splits) {
     return 1;
 }
 
+// Columns of a dense B row readable as whole float4s: N when N % 4 == 0, N
+// rounded up to 4 when the row stride leaves room (padded planes), else 0.
+int n_vec_of(const GemmArgs &g) {
+    const int n4 = (g.N + 3) & ~3;
+    return g.N % 4 == 0 ? g.N : (g.ldb >= n4 ? n4 : 0);
+}
+
 // The direct-to-LDS kernel applies to dense k-major operands with 4-aligned
 // extents and 16-byte aligned bases (PPDL_GEMM_DMA=0 turns it off).
 bool dma_ok(const GemmArgs &g) {
@@ -820,7 +830,7 @@ bool dma_ok(const GemmArgs &g) {
         return e && e[0] == '0';
     }();
     const auto a16 = [](const void *p) { return (((uintptr_t)p) & 15) == 0; };
-    return !off && !g.a_rowmajor && g.M >= 4 && g.N >= 4 && g.M % 4 == 0 && g.N % 4 == 0 && g.lda % 4 == 0 &&
+    return !off && !g.a_rowmajor && g.M >= 4 && g.M % 4 == 0 && n_vec_of(g) >= 4 && g.lda % 4 == 0 &&
            g.ldb % 4 == 0 && g.sA % 4 == 0 && g.sB % 4 == 0 && a16(g.A) && a16(g.B);
 }
 
@@ -879,7 +889,9 @@ hipError_t launch_small(const GemmArgs &g, hipStream_t s) {
 }
 
 template <int BMODE>
-hipError_t dispatch(const GemmArgs &g, const GemmWorkspace &ws, hipStream_t s) {
+hipError_t dispatch(const GemmArgs &g_in, const GemmWorkspace &ws, hipStream_t s) {
+    GemmArgs g = g_in;
+    g.n_vec = BMODE == 0 ? n_vec_of(g) : 0;
     const GemmPlan p = gemm_plan(g, ws.bytes, BMODE == 1);
     if (BMODE == 0 && p.cfg == kCfgSmall) {
         if (g.a_rowmajor && (g.K % 4 != 0 || g.lda % 4 != 0 || (((uintptr_t)g.A) & 15) != 0))

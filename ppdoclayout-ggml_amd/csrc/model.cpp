@@ -86,6 +86,15 @@ ppdl_tview view(const void *d, std::vector<int64_t> ne, int32_t type = PPDL_TYPE
 }
 ppdl_tview view(const Img &x) { return view(x.d, {x.W, x.H, x.C}); }
 
+// Winograd planes ne(T, C, 36) with rows padded to ldt tiles
+ppdl_tview planes(const float *d, int64_t T, int64_t C, int64_t ldt) {
+    ppdl_tview v = view(d, {T, C, 36});
+    v.nb[1] = ldt * 4;
+    v.nb[2] = v.nb[1] * C;
+    v.nb[3] = v.nb[2] * 36;
+    return v;
+}
+
 std::vector<int32_t> op_params(int op, int p14, int p15) {
     std::vector<int32_t> v(16, 0);
     v[12] = (int32_t)PPDL_MAGIC;
@@ -419,8 +428,11 @@ Img Net::conv(const Img &x, const std::string &name, int s, int p, int act, floa
     } else if (K == 3 && s == 1 && p == 1 && pad_end == 0 && add_mode == 0) {
         // Winograd F(4,3): pad fused into op 15, madd (op 12), output + bias + act (op 11) (:425-463)
         const int TW = (OW + 3) / 4, TH = (OH + 3) / 4, T = TW * TH;
+        // plane rows padded to a multiple of 4 tiles: the madd GEMM then reads
+        // whole float4s (and may copy them straight to LDS) on every tile
+        const int ldt = (T + 3) & ~3;
         Scratch *sc = &sc_[lane_];
-        sc->wg_need = std::max(sc->wg_need, (int64_t)36 * std::max(x.C, OC) * T);
+        sc->wg_need = std::max(sc->wg_need, (int64_t)36 * std::max(x.C, OC) * ldt);
         // The 36-plane intermediates dt / yt are shared by every Winograd
         // conv and allocated once the largest is known, so the launches
         // read their address at run time.  The workspace query only reads
@@ -429,18 +441,18 @@ Img Net::conv(const Img &x, const std::string &name, int s, int p, int act, floa
         const float *wg4 = W(name + ".wg4");
         const auto p_in = op_params(PPDL_OP_WG4_INPUT_PAD, T, TH), p_md = op_params(PPDL_OP_WG4_MADD, 0, 0),
                    p_out = op_params(PPDL_OP_WG4_OUTPUT, act, TW);
-        const ppdl_tview qd = view(kShapeOnly, {T, OC, 36});
-        const ppdl_tview qs[2] = {view(kShapeOnly, {T, x.C, 36}), view(wg4, {OC, x.C, 36})};
+        const ppdl_tview qd = planes(kShapeOnly, T, OC, ldt);
+        const ppdl_tview qs[2] = {planes(kShapeOnly, T, x.C, ldt), view(wg4, {OC, x.C, 36})};
         const int64_t wsb = ppdl_hip_workspace_bytes(p_md.data(), &qd, qs, 2);
         if (wsb < 0 && bad_node_.empty()) bad_node_ = name;
         sc->ws_need = std::max(sc->ws_need, wsb);
         node(name + ".wg_in", 1, [=](hipStream_t st) {
-            ppdl_tview d = view(sc->dt, {T, xi.C, 36}), sx = view(xi);
+            ppdl_tview d = planes(sc->dt, T, xi.C, ldt), sx = view(xi);
             return ppdl_hip_run(p_in.data(), &d, &sx, 1, st);
         });
         node(name + ".wg_madd", wsb > 0 ? 2 : 1, [=](hipStream_t st) {
-            ppdl_tview d = view(sc->yt, {T, OC, 36});
-            std::vector<ppdl_tview> sv = {view(sc->dt, {T, xi.C, 36}), view(wg4, {OC, xi.C, 36})};
+            ppdl_tview d = planes(sc->yt, T, OC, ldt);
+            std::vector<ppdl_tview> sv = {planes(sc->dt, T, xi.C, ldt), view(wg4, {OC, xi.C, 36})};
             if (wsb > 0) sv.push_back(view(sc->ws, {(sc->ws_bytes + 3) / 4}));
             return ppdl_hip_run(p_md.data(), &d, sv.data(), (int)sv.size(), st);
         });
@@ -451,7 +463,7 @@ Img Net::conv(const Img &x, const std::string &name, int s, int p, int act, floa
         }
         node(name + ".wg_out", 1, [=](hipStream_t st) {
             ppdl_tview d = view(y);
-            ppdl_tview sv[2] = {view(sc->yt, {T, OC, 36}), view(b, {OC})};
+            ppdl_tview sv[2] = {planes(sc->yt, T, OC, ldt), view(b, {OC})};
             return ppdl_hip_run(p_out.data(), &d, sv, 2, st);
         });
     } else {

@@ -3,6 +3,8 @@
 // interpolation, layer norm, attention, elementwise), written for gfx950.
 // Semantics follow the ggml ops the reference graph calls
 // (src/ppdoclayout.cpp:363-883); each kernel cites its call site.
+#include <algorithm>
+
 #include "net_internal.h"
 
 #pragma clang fp contract(off)
@@ -20,30 +22,50 @@ __device__ __forceinline__ float act_f(float v, int act) {
 
 // ---------------------------------------------------------------------------
 // Depthwise conv + bias + act (ggml_conv_2d_dw_direct + add + act,
-// src/ppdoclayout.cpp:400-404).  One thread per output pixel, taps summed in
-// (kh, kw) order.  w: [C][K][K].
+// src/ppdoclayout.cpp:400-404).  w: [C][K][K].  A block owns one channel and
+// a band of RB output rows: it stages the band's input rows, zero-padded by P
+// on every side, in LDS with coalesced loads, then each thread sums the K*K
+// taps of its outputs in (kh, kw) order from LDS (K is a template argument:
+// the taps are unrolled and their reads issued together).  A padding tap adds
+// fmaf(0, w, s) = s, so the sum equals the one over in-bounds taps only.
+// Bands are sized for ~2048 blocks so that enough waves hide LDS latency.
+constexpr int kDwLds = 8192;  // floats of staged input per block
+
+template <int K>
 __global__ __launch_bounds__(256) void k_dwconv(const float *__restrict__ x, const float *__restrict__ w,
                                                 const float *__restrict__ b, float *__restrict__ out, int C,
-                                                int IH, int IW, int OH, int OW, int K, int S, int P, int act) {
-    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    const int64_t total = (int64_t)C * OH * OW;
-    if (idx >= total) return;
-    const int c = (int)(idx / ((int64_t)OH * OW));
-    const int rem = (int)(idx - (int64_t)c * OH * OW);
-    const int oy = rem / OW, ox = rem - oy * OW;
-    const float *xc = x + (int64_t)c * IH * IW;
-    const float *wc = w + (int64_t)c * K * K;
-    float s = 0.0f;
-    for (int kh = 0; kh < K; kh++) {
-        const int iy = oy * S + kh - P;
-        if (iy < 0 || iy >= IH) continue;
-        for (int kw = 0; kw < K; kw++) {
-            const int ix = ox * S + kw - P;
-            if (ix < 0 || ix >= IW) continue;
-            s = fmaf(xc[(int64_t)iy * IW + ix], wc[kh * K + kw], s);
-        }
+                                                int IH, int IW, int OH, int OW, int S, int P, int act, int RB) {
+    __shared__ float tile[kDwLds];
+    const int c = blockIdx.y, oy0 = blockIdx.x * RB;
+    const int rows = min(RB, OH - oy0);
+    const int TR = (rows - 1) * S + K, TC = IW + 2 * P;  // staged rows / columns
+    const int iy0 = oy0 * S - P;
+    const float *__restrict__ xc = x + (int64_t)c * IH * IW;
+    for (int i = threadIdx.x; i < TR * TC; i += 256) {
+        const int r = i / TC, col = i - r * TC;
+        const int iy = iy0 + r, ix = col - P;
+        tile[i] = (iy >= 0 && iy < IH && ix >= 0 && ix < IW) ? xc[(int64_t)iy * IW + ix] : 0.0f;
     }
-    out[idx] = act_f(s + b[c], act);
+    __syncthreads();
+    const float *__restrict__ wc = w + (int64_t)c * K * K;
+    float wk[K * K];
+#pragma unroll
+    for (int i = 0; i < K * K; i++) wk[i] = wc[i];
+    const float bc = b[c];
+    float *__restrict__ oc = out + (int64_t)c * OH * OW + (int64_t)oy0 * OW;
+    for (int o = threadIdx.x; o < rows * OW; o += 256) {
+        const int oy = o / OW, ox = o - oy * OW;
+        const float *t = tile + oy * S * TC + ox * S;
+        float v[K * K];
+#pragma unroll
+        for (int kh = 0; kh < K; kh++)
+#pragma unroll
+            for (int kw = 0; kw < K; kw++) v[kh * K + kw] = t[kh * TC + kw];
+        float s = 0.0f;
+#pragma unroll
+        for (int i = 0; i < K * K; i++) s = fmaf(v[i], wk[i], s);
+        oc[o] = act_f(s + bc, act);
+    }
 }
 
 // 2x2 stride-1 max pool of x zero-padded by one column and one row at the
@@ -151,8 +173,9 @@ __global__ __launch_bounds__(256) void k_layernorm(const float *__restrict__ a, 
 // q, k, v are token-major with row strides ldq/ldk/ldv.
 //
 // On the FP32 matrix cores (v_mfma_f32_32x32x2_f32).  A block owns one head
-// and 32 queries; its 4 waves take interleaved 32-key chunks and keep an
-// online softmax each, merged at the end.  Per chunk a wave computes the
+// and 32 queries; its 8 waves take interleaved 32-key chunks and keep an
+// online softmax each, merged at the end (the merge buffers reuse the K/V
+// staging space once every wave is done with it).  Per chunk a wave computes the
 // transposed scores S^T = K Q^T (32 keys x 32 queries), so each lane's
 // accumulator column is one query: the row max / sum over keys stay within a
 // lane pair, and the accumulator registers of S^T are directly the B operand
@@ -161,16 +184,17 @@ __global__ __launch_bounds__(256) void k_layernorm(const float *__restrict__ a, 
 // K and V chunks pass through a per-wave LDS slice; no block barrier until
 // the merge.
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
-constexpr int kAttQ = 32, kAttWaves = 4;
+constexpr int kAttQ = 32, kAttWaves = 8, kAttThreads = 64 * kAttWaves;
 
-__global__ __launch_bounds__(256) void k_attention(const float *__restrict__ q, int ldq,
-                                                   const float *__restrict__ k, int ldk,
-                                                   const float *__restrict__ v, int ldv, float *__restrict__ out,
-                                                   int ldo, int T, float scale) {
-    __shared__ float Ks[kAttWaves][32][kHD + 1];
-    __shared__ float Vs[kAttWaves][32][kHD + 1];
+__global__ __launch_bounds__(kAttThreads) void k_attention(const float *__restrict__ q, int ldq,
+                                                           const float *__restrict__ k, int ldk,
+                                                           const float *__restrict__ v, int ldv,
+                                                           float *__restrict__ out, int ldo, int T, float scale) {
+    __shared__ float stage[2][kAttWaves][32][kHD + 1];  // K and V chunks per wave; then the merge tiles
     __shared__ float mw[kAttWaves][kAttQ], lw[kAttWaves][kAttQ];
-    __shared__ float ow[kAttWaves][kHD][kAttQ + 1];
+    float (*Ks)[32][kHD + 1] = stage[0];
+    float (*Vs)[32][kHD + 1] = stage[1];
+    float (*ow)[kHD][kAttQ + 1] = stage[0];  // [wave][d][q], valid after the loop barrier
     const int h = blockIdx.y, q0 = blockIdx.x * kAttQ;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int l32 = lane & 31, hi = lane >> 5;
@@ -249,6 +273,7 @@ __global__ __launch_bounds__(256) void k_attention(const float *__restrict__ q, 
     }
 
     // merge the waves' partial softmaxes
+    __syncthreads();  // every wave is done with its K/V slice (ow aliases it)
     if (hi == 0) {
         mw[wave][l32] = m;
         lw[wave][l32] = lsum;
@@ -258,8 +283,8 @@ __global__ __launch_bounds__(256) void k_attention(const float *__restrict__ q, 
     __syncthreads();
     const int d = threadIdx.x & 31;
 #pragma unroll
-    for (int j = 0; j < kAttQ / 8; j++) {
-        const int qi = (threadIdx.x >> 5) + 8 * j, t = q0 + qi;
+    for (int j = 0; j < kAttQ * 32 / kAttThreads; j++) {
+        const int qi = (threadIdx.x >> 5) + (kAttThreads / 32) * j, t = q0 + qi;
         float M = -INFINITY;
 #pragma unroll
         for (int w = 0; w < kAttWaves; w++) M = fmaxf(M, mw[w][qi]);
@@ -349,8 +374,17 @@ unsigned blocks_for(int64_t n) { return (unsigned)((n + 255) / 256); }
 hipError_t dwconv(const float *x, const float *w, const float *b, float *out, int C, int IH, int IW, int K, int S,
                   int P, int act, hipStream_t s) {
     const int OH = (IH + 2 * P - K) / S + 1, OW = (IW + 2 * P - K) / S + 1;
-    hipLaunchKernelGGL(k_dwconv, dim3(blocks_for((int64_t)C * OH * OW)), dim3(256), 0, s, x, w, b, out, C, IH,
-                       IW, OH, OW, K, S, P, act);
+    const int TC = IW + 2 * P;
+    // the band's staged rows must fit the LDS tile: (RB - 1) * S + K rows of TC
+    const int max_rows = kDwLds / TC;
+    if (C < 1 || OH < 1 || OW < 1 || C > 65535 || max_rows < K || (K != 3 && K != 5)) return hipErrorInvalidValue;
+    const int bands = std::max(1, (2048 + C - 1) / C);
+    const int RB = std::max(1, std::min((OH + bands - 1) / bands, (max_rows - K) / S + 1));
+    const dim3 grid((OH + RB - 1) / RB, C);
+    if (K == 3)
+        hipLaunchKernelGGL(k_dwconv<3>, grid, dim3(256), 0, s, x, w, b, out, C, IH, IW, OH, OW, S, P, act, RB);
+    else
+        hipLaunchKernelGGL(k_dwconv<5>, grid, dim3(256), 0, s, x, w, b, out, C, IH, IW, OH, OW, S, P, act, RB);
     return hipGetLastError();
 }
 
@@ -376,7 +410,7 @@ hipError_t attention(const float *q, int ldq, const float *k, int ldk, const flo
                      int ldo, int T, hipStream_t s) {
     // K and V rows are read as float4
     if (T < 1 || ldk % 4 || ldv % 4 || (((uintptr_t)k | (uintptr_t)v) & 15)) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_attention, dim3((T + kAttQ - 1) / kAttQ, kNH), dim3(256), 0, s, q, ldq, k, ldk, v, ldv,
+    hipLaunchKernelGGL(k_attention, dim3((T + kAttQ - 1) / kAttQ, kNH), dim3(kAttThreads), 0, s, q, ldq, k, ldk, v, ldv,
                        out, ldo, T, 1.0f / sqrtf((float)kHD));
     return hipGetLastError();
 }

@@ -68,6 +68,9 @@ struct GemmArgs {
     // choosing OW/OH), k = (kh*KW + kw)*IC + ic, n = oy*OW + ox
     int IC, IH, IW, OW, KW, S, P;
     int a_rowmajor, bias_n, c_trans, add_mode;
+    // set by the dispatcher: B rows readable as whole float4s up to this
+    // column (N itself, or N rounded up to 4 when ldb leaves room), 0 if not
+    int n_vec;
     const float *add;
 };
 
@@ -97,10 +100,11 @@ hipError_t gemm_im2col(const GemmArgs &g, const GemmWorkspace &ws, hipStream_t s
 
 // ---- Winograd transforms ----
 // pad: 0 when x is already padded (op 10), 1 when the conv's pad is fused.
-hipError_t wg4_input(const float *x, float *dt, int IW, int IH, int IC, int TW, int TH, int pad,
+// dt / yt planes: [36][C][ldt] with the T = TW*TH tiles first in each row
+hipError_t wg4_input(const float *x, float *dt, int IW, int IH, int IC, int TW, int TH, int pad, int ldt,
                      hipStream_t s);
 hipError_t wg4_output(const float *yt, const float *bias, float *out, int TW, int TH, int OC,
-                      int OW, int OH, int act, hipStream_t s);
+                      int OW, int OH, int act, int ldt, hipStream_t s);
 
 // ---- elementwise / data movement ----
 hipError_t bias_act(const float *in, const float *bias, float *out, int64_t n, int64_t plane,

@@ -72,6 +72,15 @@ bool rows_f32(const ppdl_tview *t) {
     return t->ne[2] == 1 && t->ne[3] == 1;
 }
 
+// F32 Winograd planes ne(T, C, 36, 1): rows of T tiles with a row stride
+// nb[1] >= 4T (a multiple of 4 bytes), planes packed after the C rows
+bool planes_f32(const ppdl_tview *t, int64_t T, int64_t C) {
+    if (!t || !t->data || t->type != PPDL_TYPE_F32 || t->nb[0] != 4) return false;
+    if (t->ne[0] != T || t->ne[1] != C || t->ne[2] != 36 || t->ne[3] != 1) return false;
+    if (t->nb[1] < T * 4 || t->nb[1] % 4 != 0 || t->nb[2] != t->nb[1] * C || t->nb[3] != t->nb[2] * 36) return false;
+    return t->nb[3] / 4 <= kMaxI32;
+}
+
 bool ws_valid(const ppdl_tview *t) {
     if (!t->data || (t->type != PPDL_TYPE_F32 && t->type != PPDL_TYPE_I32) || t->nb[0] != 4) return false;
     for (int i = 1; i < 4; i++)
@@ -128,12 +137,12 @@ int check_op(const int32_t *p, const ppdl_tview *dst, const ppdl_tview *src, int
         }
         case PPDL_OP_WG4_INPUT:
         case PPDL_OP_WG4_INPUT_PAD: {
-            if (nsrc < 1 || !contig_f32(dst) || !contig_f32(&src[0])) return PPDL_EINVAL;
+            if (nsrc < 1 || !contig_f32(&src[0])) return PPDL_EINVAL;
             const ppdl_tview *x = &src[0];
             const int64_t T = p[14], TH = p[15];
             if (T < 1 || TH < 1 || T % TH != 0) return PPDL_EINVAL;
             const int64_t TW = T / TH, IC = x->ne[2];
-            if (x->ne[3] != 1 || !shape_is(dst, T, IC, 36, 1)) return PPDL_EINVAL;
+            if (x->ne[3] != 1 || !planes_f32(dst, T, IC)) return PPDL_EINVAL;
             if (T * IC > kMaxI32) return PPDL_EINVAL;
             if (p[13] == PPDL_OP_WG4_INPUT) {
                 // the padded frame must hold every 6x6 patch
@@ -144,21 +153,18 @@ int check_op(const int32_t *p, const ppdl_tview *dst, const ppdl_tview *src, int
             return PPDL_OK;
         }
         case PPDL_OP_WG4_MADD: {
-            if (nsrc < 2 || !contig_f32(dst) || !contig_f32(&src[0]) || !contig_f32(&src[1]))
-                return PPDL_EINVAL;
+            if (nsrc < 2 || !contig_f32(&src[1])) return PPDL_EINVAL;
             const int64_t T = src[0].ne[0], IC = src[0].ne[1], OC = src[1].ne[0];
-            if (!shape_is(&src[0], T, IC, 36, 1) || !shape_is(&src[1], OC, IC, 36, 1) ||
-                !shape_is(dst, T, OC, 36, 1))
+            if (!planes_f32(&src[0], T, IC) || !shape_is(&src[1], OC, IC, 36, 1) || !planes_f32(dst, T, OC))
                 return PPDL_EINVAL;
             if (T > kMaxI32 || IC > kMaxI32 || OC > kMaxI32) return PPDL_EINVAL;
             return PPDL_OK;
         }
         case PPDL_OP_WG4_OUTPUT: {
-            if (nsrc < 2 || !contig_f32(dst) || !contig_f32(&src[0]) || !contig_f32(&src[1]))
-                return PPDL_EINVAL;
+            if (nsrc < 2 || !contig_f32(dst) || !contig_f32(&src[1])) return PPDL_EINVAL;
             const int64_t OW = dst->ne[0], OH = dst->ne[1], OC = dst->ne[2];
             const int64_t TW = (OW + 3) / 4, TH = (OH + 3) / 4;
-            if (dst->ne[3] != 1 || !shape_is(&src[0], TW * TH, OC, 36, 1)) return PPDL_EINVAL;
+            if (dst->ne[3] != 1 || !planes_f32(&src[0], TW * TH, OC)) return PPDL_EINVAL;
             if (p[15] != TW || nelem(&src[1]) != OC || p[14] < 0 || p[14] > 2) return PPDL_EINVAL;
             return PPDL_OK;
         }
@@ -245,11 +251,11 @@ bool args_of_node(const int32_t *p, const ppdl_tview *dst, const ppdl_tview *src
             g->lda = OC;
             g->sA = IC * OC;
             g->B = (const float *)src[0].data;
-            g->ldb = T;
-            g->sB = IC * T;
+            g->ldb = src[0].nb[1] / 4;
+            g->sB = IC * g->ldb;
             g->C = (float *)dst->data;
-            g->ldc = T;
-            g->sC = OC * T;
+            g->ldc = dst->nb[1] / 4;
+            g->sC = OC * g->ldc;
             g->M = (int)OC;
             g->N = (int)T;
             g->K = (int)IC;
@@ -350,13 +356,13 @@ extern "C" PPDL_HIP_API int ppdl_hip_run(const int32_t op_params[16], const ppdl
             const int T = p[14], TH = p[15], TW = T / TH;
             return status_of(wg4_input((const float *)x->data, (float *)dst->data, (int)x->ne[0],
                                        (int)x->ne[1], (int)x->ne[2], TW, TH,
-                                       p[13] == PPDL_OP_WG4_INPUT_PAD ? 1 : 0, s));
+                                       p[13] == PPDL_OP_WG4_INPUT_PAD ? 1 : 0, (int)(dst->nb[1] / 4), s));
         }
         case PPDL_OP_WG4_OUTPUT: {
             const int OW = (int)dst->ne[0], OH = (int)dst->ne[1], OC = (int)dst->ne[2];
             return status_of(wg4_output((const float *)src[0].data, (const float *)src[1].data,
                                         (float *)dst->data, (OW + 3) / 4, (OH + 3) / 4, OC, OW, OH,
-                                        p[14], s));
+                                        p[14], (int)(src[0].nb[1] / 4), s));
         }
         case PPDL_OP_MSDEF:
             return status_of(msdeform((const float *)src[0].data, (int)(src[0].nb[1] / 4), (const float *)src[1].data,

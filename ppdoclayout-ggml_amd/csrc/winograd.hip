@@ -9,7 +9,9 @@
 //
 // Both transforms are HBM-bound: one thread per (channel, tile), consecutive
 // threads on consecutive tiles, so every plane store (input transform) and
-// every plane load (output transform) is a contiguous run along t.  The
+// every plane load (output transform) is a contiguous run along t.  A plane
+// row (one channel's T tiles) may be padded to a stride ldt >= T; the
+// padding is never written by the input transform nor read by the output.  The
 // arithmetic is a fixed chain of fmaf over the nonzero matrix entries in
 // ascending index order, which the CPU oracle repeats exactly.
 #include "ppdl_internal.h"
@@ -30,7 +32,7 @@ __device__ __forceinline__ float act_f(float v, int act) {
 template <int PAD>
 __global__ __launch_bounds__(kThreads) void k_wg4_input(const float *__restrict__ x,
                                                         float *__restrict__ dt, int IW, int IH,
-                                                        int IC, int TW, int TH) {
+                                                        int IC, int TW, int TH, int ldt) {
     const int T = TW * TH;
     const int64_t idx = (int64_t)blockIdx.x * kThreads + threadIdx.x;
     if (idx >= (int64_t)T * IC) return;
@@ -64,8 +66,8 @@ __global__ __launch_bounds__(kThreads) void k_wg4_input(const float *__restrict_
                 if (kBt[u][a] != 0.0f) s = fmaf(kBt[u][a], d[a][b], s);
             t1[u][b] = s;
         }
-    float *__restrict__ o = dt + (int64_t)ic * T + tile;
-    const int64_t pstride = (int64_t)IC * T;
+    float *__restrict__ o = dt + (int64_t)ic * ldt + tile;
+    const int64_t pstride = (int64_t)IC * ldt;
 #pragma unroll
     for (int u = 0; u < 6; u++)
 #pragma unroll
@@ -81,7 +83,7 @@ __global__ __launch_bounds__(kThreads) void k_wg4_input(const float *__restrict_
 __global__ __launch_bounds__(kThreads) void k_wg4_output(const float *__restrict__ yt,
                                                          const float *__restrict__ bias,
                                                          float *__restrict__ out, int TW, int TH,
-                                                         int OC, int OW, int OH, int act) {
+                                                         int OC, int OW, int OH, int act, int ldt) {
     const int T = TW * TH;
     const int64_t idx = (int64_t)blockIdx.x * kThreads + threadIdx.x;
     if (idx >= (int64_t)T * OC) return;
@@ -89,8 +91,8 @@ __global__ __launch_bounds__(kThreads) void k_wg4_output(const float *__restrict
     const int tile = (int)(idx - (int64_t)oc * T);
     const int ty = tile / TW, tx = tile - ty * TW;
 
-    const float *__restrict__ src = yt + (int64_t)oc * T + tile;
-    const int64_t pstride = (int64_t)OC * T;
+    const float *__restrict__ src = yt + (int64_t)oc * ldt + tile;
+    const int64_t pstride = (int64_t)OC * ldt;
     float m[6][6];
 #pragma unroll
     for (int p = 0; p < 36; p++) m[p / 6][p % 6] = src[p * pstride];
@@ -140,23 +142,23 @@ __global__ __launch_bounds__(kThreads) void k_wg4_output(const float *__restrict
 
 }  // namespace
 
-hipError_t wg4_input(const float *x, float *dt, int IW, int IH, int IC, int TW, int TH, int pad,
+hipError_t wg4_input(const float *x, float *dt, int IW, int IH, int IC, int TW, int TH, int pad, int ldt,
                      hipStream_t s) {
     const int64_t n = (int64_t)TW * TH * IC;
     const unsigned blocks = (unsigned)((n + kThreads - 1) / kThreads);
     if (pad)
-        hipLaunchKernelGGL(k_wg4_input<1>, dim3(blocks), dim3(kThreads), 0, s, x, dt, IW, IH, IC, TW, TH);
+        hipLaunchKernelGGL(k_wg4_input<1>, dim3(blocks), dim3(kThreads), 0, s, x, dt, IW, IH, IC, TW, TH, ldt);
     else
-        hipLaunchKernelGGL(k_wg4_input<0>, dim3(blocks), dim3(kThreads), 0, s, x, dt, IW, IH, IC, TW, TH);
+        hipLaunchKernelGGL(k_wg4_input<0>, dim3(blocks), dim3(kThreads), 0, s, x, dt, IW, IH, IC, TW, TH, ldt);
     return hipGetLastError();
 }
 
 hipError_t wg4_output(const float *yt, const float *bias, float *out, int TW, int TH, int OC,
-                      int OW, int OH, int act, hipStream_t s) {
+                      int OW, int OH, int act, int ldt, hipStream_t s) {
     const int64_t n = (int64_t)TW * TH * OC;
     const unsigned blocks = (unsigned)((n + kThreads - 1) / kThreads);
     hipLaunchKernelGGL(k_wg4_output, dim3(blocks), dim3(kThreads), 0, s, yt, bias, out, TW, TH, OC,
-                       OW, OH, act);
+                       OW, OH, act, ldt);
     return hipGetLastError();
 }
 

@@ -96,6 +96,38 @@ def hip_winograd(hip, x, w, b, act, prepadded=False, use_ws=True):
     return out, dt, yt, wg4
 
 
+def planes_view(hip, t, T, C):
+    """ppdl_tview ne(T, C, 36) over a torch (36, C, ldt) buffer: rows padded."""
+    ldt = t.shape[2]
+    v = hip.TView()
+    v.data = t.data_ptr()
+    for i, (n, b) in enumerate(zip((T, C, 36, 1), (4, ldt * 4, ldt * 4 * C, ldt * 4 * C * 36))):
+        v.ne[i], v.nb[i] = n, b
+    v.type = hip.TYPE_F32
+    return v
+
+
+def hip_winograd_padded(hip, x, w, b, act, ldt):
+    """ops 15 -> 12 -> 11 with dt / yt plane rows padded to ldt (padding NaN)."""
+    IC, H, W = x.shape
+    OC = w.shape[0]
+    TW, TH = (W + 3) // 4, (H + 3) // 4
+    T = TW * TH
+    _, wg4 = hip.repack_conv(w)
+    dt = torch.full((36, IC, ldt), float("nan"), device="cuda")
+    yt = torch.full((36, OC, ldt), float("nan"), device="cuda")
+    out = torch.empty((OC, H, W), device="cuda")
+    vdt, vyt = planes_view(hip, dt, T, IC), planes_view(hip, yt, T, OC)
+    hip.run_checked(hip.OP_WG4_INPUT_PAD, vdt, [dev(x)], T, TH)
+    srcs = [vdt, dev(wg4)]
+    nb = hip.workspace_bytes(hip.OP_WG4_MADD, vyt, srcs)
+    if nb > 0:
+        srcs.append(hip.make_workspace(nb))
+    hip.run_checked(hip.OP_WG4_MADD, vyt, srcs)
+    hip.run_checked(hip.OP_WG4_OUTPUT, out, [vyt, dev(b)], act, TW)
+    return out, dt
+
+
 def hip_conv_im2col(hip, x, w, b, K, S, P, act, use_ws=True):
     wr, _ = hip.repack_conv(w)
     IC, IH, IW = x.shape
@@ -165,6 +197,25 @@ def test_small_gemm_kernel(hip, orc, IC, H, W, OC, monkeypatch):
 
 
 # ---------------------------------------------------------------- Winograd F(4,3)
+@pytest.mark.parametrize("IC,H,W,OC", [(64, 100, 100, 48), (96, 50, 50, 96), (256, 25, 25, 256), (7, 9, 11, 5)])
+def test_winograd_padded_planes(hip, orc, IC, H, W, OC):
+    """dt / yt plane rows padded past T (NaN-filled padding): the padding is
+    never read into a stored output, and the result equals the contiguous
+    layout's bit for bit (same kernels, same summation order)."""
+    say(f"F(4,3) padded planes {IC}->{OC} @{H}x{W}")
+    rng = np.random.default_rng(IC + H + OC)
+    x, w, b = conv_inputs(rng, IC, H, W, OC, 3)
+    T = ((W + 3) // 4) * ((H + 3) // 4)
+    ref_out = host(hip_winograd(hip, x, w, b, 2)[0])
+    for ldt in ((T + 3) // 4 * 4, T + 17):
+        out, dt = hip_winograd_padded(hip, x, w, b, 2, ldt)
+        y = host(out)
+        assert np.isfinite(y).all()
+        assert np.array_equal(y, ref_out), ldt
+        assert normwise(y, orc.conv2d_ref(x, w, b, 1, 1, 2)) < TOL
+        if ldt > T:
+            assert torch.isnan(dt[:, :, T:]).all().item()  # the input transform leaves the padding alone
+
 WG_CONFIGS = [(256, 100, 100), (256, 50, 50), (256, 25, 25), (48, 200, 200), (96, 100, 100)]
 
 
