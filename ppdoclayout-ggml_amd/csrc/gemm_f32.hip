@@ -30,6 +30,7 @@
 //
 // No TF32/bf16 emulation anywhere: products and accumulation are IEEE fp32 in
 // the matrix core; split partials are summed in fp32.
+#include <algorithm>
 #include <cstdio>
 #include <cstdlib>
 #include <type_traits>
@@ -488,9 +489,11 @@ __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((((N >> 4) & 3) << 14) | (0xF << 8) | (0x7 << 4) | (N & 0xF));
 }
 
-template <int BM, int BN, int WGM, bool SPLIT>
+// NS LDS stages: NS - 1 tiles in flight while one is computed (2 when many
+// blocks share a CU, deeper when few blocks must hide copy latency alone).
+template <int BM, int BN, int WGM, bool SPLIT, int NS>
 __global__ __launch_bounds__(kThreads) void k_gemm_dma(GemmArgs g, SplitArgs sp, int tiles_m, int tiles_mn) {
-    constexpr int NS = 2;  // LDS stages: one tile computed while the next lands
+    static_assert(NS >= 2 && NS <= 4, "stages");
     constexpr int WGN = 4 / WGM, WM = BM / WGM, WN = BN / WGN, TM = WM / 32, TN = WN / 32;
     constexpr int IA = kBK * BM / 4 / kThreads, IB = kBK * BN / 4 / kThreads;  // copies per wave per tile
     constexpr int KH = kBK / 2, NP = KH / 2;
@@ -589,19 +592,22 @@ __global__ __launch_bounds__(kThreads) void k_gemm_dma(GemmArgs g, SplitArgs sp,
     if (nk > 0) {
         const int klast = kt1 - 1;
         const int ktail = K - (nk_total - 1) * kBK;  // valid rows of the global last tile
-        issue(0, kt0);
+#pragma unroll
+        for (int u = 0; u < NS - 1; u++) issue(u, min(kt0 + u, klast));
         for (int it = 0; it < nk; it += NS) {
 #pragma unroll
             for (int u = 0; u < NS; u++) {
                 if (it + u < nk) {
                     const int kt = kt0 + it + u;
-                    wait_vmcnt<(NS - 2) * (IA + IB)>();  // this wave's copies of tile kt have landed
-                    __syncthreads();                     // everyone's have; tile kt-1 is consumed
+                    // this wave's copies of tile kt have landed (NS - 2 younger
+                    // tiles may stay in flight) ...
+                    wait_vmcnt<(NS - 2) * (IA + IB)>();
+                    __syncthreads();  // ... and everyone's; tile kt-1 is consumed
                     if (kt == nk_total - 1 && ktail < kBK) {
                         for (int i = tid; i < (kBK - ktail) * BM; i += kThreads) As[u][ktail * BM + i] = 0.0f;
                         __syncthreads();
                     }
-                    issue((u + 1) % NS, min(kt + 1, klast));
+                    issue((u + NS - 1) % NS, min(kt + NS - 1, klast));  // into tile kt-1's stage
                     compute(u);
                 }
             }
@@ -609,6 +615,136 @@ __global__ __launch_bounds__(kThreads) void k_gemm_dma(GemmArgs g, SplitArgs sp,
         wait_vmcnt<0>();  // no copy may still target this block's LDS when it exits
     }
     gemm_epilogue<TM, TN, SPLIT>(acc, g, sp, split, bz, m0 + wm0, n0 + wn0, lane);
+}
+
+// ---------------------------------------------------------------------------
+// Implicit-im2col conv with an LDS-staged input patch, for convs with at most
+// 32 output channels (the stem): the gather of the generic loader costs index
+// arithmetic and a global load per element, here each input element is loaded
+// once per block with coalesced rows.  A block owns the 32 output channels of
+// one 128-pixel segment of an output row (4 waves x 32 pixels).  Per chunk of
+// CC input channels it stages the KS input rows the segment reads (zero outside
+// the image: the conv's padding) and the chunk's weights, then runs the MFMAs
+// from LDS with k = icl * KS*KS + tap inside the chunk.  Staging issues all of
+// a thread's loads before its LDS stores (one memory latency per chunk).  The
+// epilogue is bias + act, stored only inside the row.
+constexpr int kPatchFloats = 10240, kPatchAFloats = 8192;  // LDS floats per block
+
+template <int KS, int S>
+__global__ __launch_bounds__(kThreads) void k_conv_patch(GemmArgs g, int CC, int nseg) {
+    constexpr int TW = 128, PW = (TW - 1) * S + KS, TAPS = KS * KS;
+    constexpr int JP = kPatchFloats / kThreads, JA = kPatchAFloats / kThreads;
+    __shared__ float patch[kPatchFloats];
+    __shared__ float As[kPatchAFloats];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int l32 = lane & 31, hi = lane >> 5;
+    const int b = xcd_remap(blockIdx.x, gridDim.x);
+    const int oy = b / nseg, ox0 = (b - oy * nseg) * TW;
+    const int M = g.M, IC = g.IC, IH = g.IH, IW = g.IW, OW = g.OW, lda = (int)g.lda;
+    const int KC = TAPS * CC, KCp = (KC + 1) & ~1;
+    const int iy0 = oy * S - g.P, ix0 = ox0 * S - g.P;
+    const float *__restrict__ X = g.B;
+    const float *__restrict__ A = g.A;
+    f32x16 acc;
+#pragma unroll
+    for (int r = 0; r < 16; r++) acc[r] = 0.0f;
+    const int nb = wave * 32 + l32;  // this lane's output column within the segment
+    const float *pb = patch + nb * S;
+
+    for (int ic0 = 0; ic0 < IC; ic0 += CC) {
+        const int cc = min(CC, IC - ic0);
+        const int np = cc * KS * PW, na = KCp * 32;
+        float vp[JP], va[JA];
+        // Every load is unconditional, at an address clamped into the same
+        // row / matrix (one basic block, so the loads stay in flight together;
+        // clamping to nearby addresses keeps masked lanes off any shared
+        // line), and the mask is applied to the value.
+#pragma unroll
+        for (int j = 0; j < JP; j++) {
+            const int i = min(tid + j * kThreads, np - 1);
+            const int row = i / PW, c = i - row * PW;  // row = icl * KS + r
+            const int icl = row / KS, r = row - icl * KS;
+            const int iy = iy0 + r, ix = ix0 + c;
+            const bool in = tid + j * kThreads < np && iy >= 0 && iy < IH && ix >= 0 && ix < IW;
+            const float v = X[(uint32_t)((ic0 + icl) * IH * IW + min(max(iy, 0), IH - 1) * IW + min(max(ix, 0), IW - 1))];
+            vp[j] = in ? v : 0.0f;
+        }
+#pragma unroll
+        for (int j = 0; j < JA; j++) {
+            const int i = tid + j * kThreads;
+            const int k = min(i >> 5, KC - 1), m = i & 31;
+            const int icl = k / TAPS, tap = k - icl * TAPS;
+            const bool in = i < na && (i >> 5) < KC && m < M && icl < cc;
+            const float v = A[(uint32_t)((tap * IC + ic0 + min(icl, cc - 1)) * lda + min(m, M - 1))];
+            va[j] = in ? v : 0.0f;
+        }
+        __syncthreads();  // the previous chunk is consumed
+#pragma unroll
+        for (int j = 0; j < JP; j++) {
+            if (tid + j * kThreads < np) patch[tid + j * kThreads] = vp[j];
+        }
+#pragma unroll
+        for (int j = 0; j < JA; j++) {
+            if (tid + j * kThreads < na) As[tid + j * kThreads] = va[j];
+        }
+        __syncthreads();
+        // this lane's k = 2*st + hi, stepped by 2 (TAPS is a constant); the
+        // pad row k = KC of an odd KC has zero weights and reads offset 0
+        int kk = hi, icl = 0, tap = hi;
+#pragma unroll 4
+        for (int st = 0; st < KCp / 2; st++) {
+            const int kh = tap / KS, kw = tap - kh * KS;
+            const int off = kk < KC ? (icl * KS + kh) * PW + kw : 0;
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(As[kk * 32 + l32], pb[off], acc, 0, 0, 0);
+            kk += 2;
+            tap += 2;
+            if (tap >= TAPS) {  // TAPS >= 4: at most one carry
+                tap -= TAPS;
+                ++icl;
+            }
+        }
+    }
+
+    const int ox = ox0 + nb;
+    if (ox < OW) {
+        float *__restrict__ C = g.C;
+        const int64_t pix = (int64_t)oy * OW + ox;
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int m = 8 * (r >> 2) + 4 * hi + (r & 3);
+            if (m < M) C[(int64_t)m * g.ldc + pix] = act_f(acc[r] + (g.bias ? g.bias[m] : 0.0f), g.act);
+        }
+    }
+}
+
+// Patch kernel plan: channels per chunk so that the staged rows and weights fit
+// (0 = not applicable: more than 32 output channels, or another kernel shape).
+// Opt-in (PPDL_CONV_PATCH=1): at ~306 VGPRs and 72 KB of LDS it holds one wave
+// per SIMD and measured 2.5-3x slower on the 800x800 stem convolutions than
+// the generic implicit-im2col loader, which keeps several waves per SIMD.
+int patch_cc(const GemmArgs &g) {
+    const char *e = getenv("PPDL_CONV_PATCH");
+    if (!(e && e[0] == '1') || g.M > 32 || g.a_rowmajor || g.add || g.c_trans) return 0;
+    const int KS = g.KW;
+    if (!((KS == 3 && g.S == 2) || (KS == 2 && g.S == 1))) return 0;
+    const int PW = 127 * g.S + KS;
+    int cc = std::min(g.IC, kPatchFloats / (KS * PW));
+    cc = std::min(cc, (kPatchAFloats / 32 - 1) / (KS * KS));  // (KC + 1) rows of 32 weights
+    return cc >= 1 ? cc : 0;
+}
+
+hipError_t launch_patch(const GemmArgs &g, int cc, hipStream_t s) {
+    const int OH = g.N / g.OW, nseg = (g.OW + 127) / 128;
+    const int64_t blocks = (int64_t)OH * nseg;
+    // the kernel addresses the input and the weights with 32-bit offsets
+    if (blocks <= 0 || blocks > 0x7fffffff || (int64_t)g.IC * g.IH * g.IW > 0x7fffffff ||
+        (int64_t)g.KW * g.KW * g.IC * g.lda > 0x7fffffff)
+        return hipErrorInvalidValue;
+    if (g.KW == 3)
+        hipLaunchKernelGGL((k_conv_patch<3, 2>), dim3((unsigned)blocks), dim3(kThreads), 0, s, g, cc, nseg);
+    else
+        hipLaunchKernelGGL((k_conv_patch<2, 1>), dim3((unsigned)blocks), dim3(kThreads), 0, s, g, cc, nseg);
+    return hipGetLastError();
 }
 
 // Split-K fix-up: the GEMM epilogue applied to sum_{s=0..S-1} P[s], s
@@ -783,6 +919,12 @@ int64_t tiles_of(int c, int M, int N, int batch) {
 // won or tied nearly everywhere; 32-row blocks when M <= 32.  Splitting K
 // paid only when the output had too few tiles to occupy the chip: the best
 // S kept about 1000 blocks in flight with at least 6 k tiles per split.
+// integer tuning knob from the environment (planner sweeps only)
+int64_t env_int(const char *name, int64_t dflt) {
+    const char *e = getenv(name);
+    return (e && *e) ? strtoll(e, nullptr, 10) : dflt;
+}
+
 GemmPlan plan_auto(int M, int N, int K, int batch, bool im2col) {
     // Few output tiles and a small operand footprint: the small-GEMM kernel
     // (32x32 tiles, K split over the block's waves, no split-K pass).  Its
@@ -790,7 +932,9 @@ GemmPlan plan_auto(int M, int N, int K, int batch, bool im2col) {
     // 32-wide strip of the other), hence the footprint bound.
     const int64_t t64 = (int64_t)((M + 63) / 64) * ((N + 63) / 64) * batch;
     const int64_t reread = 4 * ((int64_t)M * K * ((N + 31) / 32) + (int64_t)K * N * ((M + 31) / 32)) * batch;
-    if (!im2col && t64 < 200 && reread <= ((int64_t)40 << 20)) return GemmPlan{kCfgSmall, 1};
+    static const int64_t small_t64 = env_int("PPDL_SMALL_T64", 200);
+    static const int64_t small_mb = env_int("PPDL_SMALL_MB", 40);
+    if (!im2col && t64 < small_t64 && reread <= (small_mb << 20)) return GemmPlan{kCfgSmall, 1};
     GemmPlan p{M <= 32 ? 5 : 3, 1};
     const int nk = (K + kBK - 1) / kBK;
     const int64_t tiles = tiles_of(p.cfg, M, N, batch);
@@ -834,6 +978,31 @@ bool dma_ok(const GemmArgs &g) {
            g.ldb % 4 == 0 && g.sA % 4 == 0 && g.sB % 4 == 0 && a16(g.A) && a16(g.B);
 }
 
+// LDS stages of the direct-to-LDS kernel: deeper when the launch leaves
+// fewer than ~2 blocks per CU (each block must hide its own copy latency)
+int dma_stages(int64_t blocks) {
+    static const int64_t low = env_int("PPDL_DMA_LOW_BLOCKS", 512);
+    static const int deep = (int)env_int("PPDL_DMA_NS", 2);
+    return blocks < low ? deep : 2;
+}
+
+template <int BM, int BN, int WGM, bool SPLIT>
+void launch_dma(const GemmArgs &g, const SplitArgs &sp, int64_t total, int tiles_m, int tiles_n, hipStream_t s) {
+    switch (dma_stages(total)) {
+        case 3:
+            hipLaunchKernelGGL((k_gemm_dma<BM, BN, WGM, SPLIT, 3>), dim3((unsigned)total), dim3(kThreads), 0, s, g,
+                               sp, tiles_m, tiles_m * tiles_n);
+            break;
+        case 4:
+            hipLaunchKernelGGL((k_gemm_dma<BM, BN, WGM, SPLIT, 4>), dim3((unsigned)total), dim3(kThreads), 0, s, g,
+                               sp, tiles_m, tiles_m * tiles_n);
+            break;
+        default:
+            hipLaunchKernelGGL((k_gemm_dma<BM, BN, WGM, SPLIT, 2>), dim3((unsigned)total), dim3(kThreads), 0, s, g,
+                               sp, tiles_m, tiles_m * tiles_n);
+    }
+}
+
 template <int BM, int BN, int WGM, int AMODE, int BMODE>
 hipError_t launch(const GemmArgs &g, int S, const GemmWorkspace &ws, hipStream_t s) {
     const int tiles_m = (g.M + BM - 1) / BM, tiles_n = (g.N + BN - 1) / BN;
@@ -851,8 +1020,7 @@ hipError_t launch(const GemmArgs &g, int S, const GemmWorkspace &ws, hipStream_t
         sp.ktiles_per_split = (nk + S - 1) / S;
         sp.partials = (float *)ws.base;
         if (AMODE == 0 && BMODE == 0 && dma_ok(g))
-            hipLaunchKernelGGL((k_gemm_dma<BM, BN, WGM, true>), dim3((unsigned)total), dim3(kThreads), 0, s, g, sp,
-                               tiles_m, tiles_m * tiles_n);
+            launch_dma<BM, BN, WGM, true>(g, sp, total, tiles_m, tiles_n, s);
         else
             hipLaunchKernelGGL((k_gemm<BM, BN, WGM, AMODE, BMODE, true>), dim3((unsigned)total), dim3(kThreads), 0,
                                s, g, sp, tiles_m, tiles_m * tiles_n);
@@ -867,8 +1035,7 @@ hipError_t launch(const GemmArgs &g, int S, const GemmWorkspace &ws, hipStream_t
             hipLaunchKernelGGL(k_splitk_reduce<1>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
                                sp.partials, S, n, g);
     } else if (AMODE == 0 && BMODE == 0 && dma_ok(g)) {
-        hipLaunchKernelGGL((k_gemm_dma<BM, BN, WGM, false>), dim3((unsigned)total), dim3(kThreads), 0, s, g, sp,
-                           tiles_m, tiles_m * tiles_n);
+        launch_dma<BM, BN, WGM, false>(g, sp, total, tiles_m, tiles_n, s);
     } else {
         hipLaunchKernelGGL((k_gemm<BM, BN, WGM, AMODE, BMODE, false>), dim3((unsigned)total), dim3(kThreads), 0,
                            s, g, sp, tiles_m, tiles_m * tiles_n);
@@ -892,6 +1059,8 @@ template <int BMODE>
 hipError_t dispatch(const GemmArgs &g_in, const GemmWorkspace &ws, hipStream_t s) {
     GemmArgs g = g_in;
     g.n_vec = BMODE == 0 ? n_vec_of(g) : 0;
+    if (BMODE == 1)
+        if (const int cc = patch_cc(g)) return launch_patch(g, cc, s);
     const GemmPlan p = gemm_plan(g, ws.bytes, BMODE == 1);
     if (BMODE == 0 && p.cfg == kCfgSmall) {
         if (g.a_rowmajor && (g.K % 4 != 0 || g.lda % 4 != 0 || (((uintptr_t)g.A) & 15) != 0))
@@ -948,6 +1117,7 @@ int64_t gemm_ws_bytes_for(const GemmArgs &g, bool im2col) {
 hipError_t gemm_dense(const GemmArgs &g, const GemmWorkspace &ws, hipStream_t s) { return dispatch<0>(g, ws, s); }
 
 std::string gemm_kernel_name(const GemmArgs &g, int64_t ws_bytes, bool im2col) {
+    if (im2col && patch_cc(g)) return g.KW == 3 ? "k_conv_patch<3, 2>" : "k_conv_patch<2, 1>";
     const GemmPlan p = gemm_plan(g, ws_bytes, im2col);
     if (p.cfg == kCfgSmall) return g.a_rowmajor ? "k_gemm_small<1>" : "k_gemm_small<0>";
     int bm = kCfgs[p.cfg].bm, bn = kCfgs[p.cfg].bn, wgm = kCfgs[p.cfg].wgm;

@@ -321,6 +321,38 @@ def test_conv_golden_fixtures_on_gpu(hip, orc):
         assert normwise(y, f["y"]) < TOL, path
 
 
+@pytest.mark.parametrize("IC,H,W,OC,K,S,P,PE", [
+    (3, 800, 800, 32, 3, 2, 1, 0),     # stem1
+    (32, 400, 400, 16, 2, 1, 0, 1),    # stem2a (zero pad after the last column / row)
+    (64, 200, 200, 32, 3, 2, 1, 0),    # stem3: several channel chunks
+    (37, 33, 150, 24, 3, 2, 1, 0),     # ragged: channel chunk remainder, partial row segment
+    (5, 9, 7, 3, 2, 1, 0, 1),          # tiny
+])
+def test_conv_patch_kernel(hip, orc, IC, H, W, OC, K, S, P, PE, monkeypatch):
+    """Op 16 with <= 32 output channels on the opt-in LDS-patch kernel
+    (PPDL_CONV_PATCH=1): against the oracle, and against the default generic
+    implicit-im2col loader (PPDL_CONV_PATCH=0)."""
+    say(f"patch conv {IC}->{OC} k{K}s{S} @{H}x{W} pe{PE}")
+    rng = np.random.default_rng(IC * 31 + OC + H)
+    x, w, b = conv_inputs(rng, IC, H, W, OC, K)
+    wr, _ = hip.repack_conv(w)
+    OH, OW = (H + 2 * P + PE - K) // S + 1, (W + 2 * P + PE - K) // S + 1
+    p14 = K | (S << 8) | (P << 16) | (1 << 24)
+    outs = []
+    for flag in ("1", "0"):
+        monkeypatch.setenv("PPDL_CONV_PATCH", flag)
+        out = torch.full((OC, OH, OW), float("nan"), device="cuda")
+        srcs = with_ws(hip, hip.OP_CONV_IM2COL, out, [dev(x), dev(wr), dev(b)], p14, PE, True)
+        hip.run_checked(hip.OP_CONV_IM2COL, out, srcs, p14, PE)
+        outs.append(host(out))
+    xp = np.pad(x, ((0, 0), (0, PE), (0, PE))) if PE else x
+    ref = orc.conv2d_ref(xp, w, b, S, P, 1)
+    assert np.isfinite(outs[0]).all()
+    assert normwise(outs[0], ref) < TOL
+    assert normwise(outs[1], ref) < TOL
+    assert normwise(outs[0], outs[1]) < TOL
+
+
 # ---------------------------------------------------------------- split-K
 SPLIT_SHAPES = [  # long K, few output tiles: the planner splits K
     ("conv1x1", (3328, 25, 25, 1024, 1, 1, 0)),
