@@ -783,22 +783,24 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(const float *__restrict__
 // ---------------------------------------------------------------------------
 // Small-GEMM path: for shapes whose 64x64 tiling leaves most of the chip idle
 // (the decoder's 300-token linears, the backbone's last stages).  A block owns
-// a 32x32 output tile and its 4 waves split K: wave w contracts k chunks
-// w, w+4, ... of 64.  Fragments come straight from global memory into
-// registers in MFMA operand order (no LDS staging), with the next chunk's
-// loads issued before the current chunk's MFMAs, so a wave pays about one
-// memory latency per two chunks instead of one per k tile.  The 4 partial
+// a 32x32 output tile and its WV waves split K: wave w contracts k chunks
+// w, w+WV, ... of 32, so the serial MFMA chain per wave is K/WV long (the
+// planner picks WV = 4, 8 or 16 from K).  Fragments come straight from global
+// memory into registers in MFMA operand order (no LDS staging), with the next
+// chunk's loads issued before the current chunk's MFMAs.  The WV partial
 // tiles are summed through LDS in fixed wave order (deterministic) and the
 // usual epilogue applies.
 //
-// Operand order per chunk (kb = chunk start): step s = 4c + j (c < 8, j < 4)
+// Operand order per chunk (kb = chunk start): step s = 4c + j (c < 4, j < 4)
 // pairs k = kb + 8c + j (lanes 0-31) with k = kb + 8c + 4 + j (lanes 32-63);
 // A and B use the same pairing, so the sum covers every k once.  A row-major
 // (AMODE 1) is then one float4 per lane per c.
-template <int AMODE>
-__global__ __launch_bounds__(kThreads) void k_gemm_small(GemmArgs g, int tiles_m, int tiles_mn) {
-    constexpr int KC = 64, NS = KC / 2;
-    __shared__ float red[4][32][33];
+constexpr int kSmallKC = 32;
+
+template <int AMODE, int WV>
+__global__ __launch_bounds__(WV * 64) void k_gemm_small(GemmArgs g, int tiles_m, int tiles_mn) {
+    constexpr int KC = kSmallKC, NS = KC / 2, NT = WV * 64;
+    __shared__ float red[WV][32][33];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int l32 = lane & 31, h = lane >> 5;
     const int logical = xcd_remap(blockIdx.x, gridDim.x);
@@ -815,7 +817,7 @@ __global__ __launch_bounds__(kThreads) void k_gemm_small(GemmArgs g, int tiles_m
     auto load = [&](float (&a)[NS], float (&b)[NS], int ch) {
         const int kb = ch * KC;
 #pragma unroll
-        for (int c = 0; c < 8; c++) {
+        for (int c = 0; c < KC / 8; c++) {
             const int k4 = kb + 8 * c + 4 * h;  // this lane's 4 consecutive k
             if (AMODE == 1) {
                 // K % 4 == 0: the 4 k are all inside or all outside
@@ -850,21 +852,21 @@ __global__ __launch_bounds__(kThreads) void k_gemm_small(GemmArgs g, int tiles_m
 #pragma unroll
         for (int st = 0; st < NS; st++) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[st], b[st], acc, 0, 0, 0);
     };
-    // chunks of this wave: wave, wave + 4, ...; two register stages
+    // chunks of this wave: wave, wave + WV, ...; two register stages
     int ch = wave;
     if (ch < nchunk) load(a0, b0, ch);
     while (ch < nchunk) {
-        if (ch + 4 < nchunk) load(a1, b1, ch + 4);
+        if (ch + WV < nchunk) load(a1, b1, ch + WV);
         __builtin_amdgcn_sched_barrier(0);
         mma(a0, b0);
         __builtin_amdgcn_sched_barrier(0);
-        ch += 4;
+        ch += WV;
         if (ch >= nchunk) break;
-        if (ch + 4 < nchunk) load(a0, b0, ch + 4);
+        if (ch + WV < nchunk) load(a0, b0, ch + WV);
         __builtin_amdgcn_sched_barrier(0);
         mma(a1, b1);
         __builtin_amdgcn_sched_barrier(0);
-        ch += 4;
+        ch += WV;
     }
 
     // accumulator: lane owns column l32, rows 8(r/4) + 4h + r%4
@@ -875,14 +877,16 @@ __global__ __launch_bounds__(kThreads) void k_gemm_small(GemmArgs g, int tiles_m
     const float *__restrict__ bias = g.bias;
     float *__restrict__ C = g.C + (int64_t)bz * g.sC;
     const float *__restrict__ Ad = g.add ? g.add + (int64_t)bz * g.sC : nullptr;
-    // 256 threads x 4 outputs; consecutive threads along the contiguous axis of C
+    // NT threads x 1024/NT outputs; consecutive threads along the contiguous axis of C
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int fast = tid & 31, slow = (tid >> 5) + 8 * i;
+    for (int i = 0; i < 1024 / NT; i++) {
+        const int fast = tid & 31, slow = (tid >> 5) + (NT / 32) * i;
         const int mm = g.c_trans ? fast : slow, nn = g.c_trans ? slow : fast;
         const int m = m0 + mm, n = n0 + nn;
         if (m < M && n < N) {
-            float v = ((red[0][mm][nn] + red[1][mm][nn]) + red[2][mm][nn]) + red[3][mm][nn];
+            float v = red[0][mm][nn];
+#pragma unroll
+            for (int w = 1; w < WV; w++) v += red[w][mm][nn];
             const int64_t idx = g.c_trans ? (int64_t)n * g.ldc + m : (int64_t)m * g.ldc + n;
             if (bias) v += bias[g.bias_n ? n : m];
             if (g.add_mode == 1) v += Ad[idx];
@@ -892,6 +896,25 @@ __global__ __launch_bounds__(kThreads) void k_gemm_small(GemmArgs g, int tiles_m
         }
     }
 }
+
+// Waves of the small-GEMM kernel (PPDL_SMALL_WV pins 4, 8 or 16 for sweeps
+// and tests).  Measured on the network's shapes: with 256 or more 32x32
+// tiles the grid already fills the chip and 4 waves per tile won (less LDS
+// reduction, more blocks resident); below that, splitting K as far as one or
+// two 32-k chunks per wave won (the 300-token decoder linears: 5.8 -> 4.8 us
+// at K = 256, 12.7 -> 10.9 us at K = 1024).
+int small_waves(int K, int64_t tiles) {
+    const char *e = getenv("PPDL_SMALL_WV");
+    if (e && *e) {
+        const int w = atoi(e);
+        if (w == 4 || w == 8 || w == 16) return w;
+    }
+    const int nchunk = (K + kSmallKC - 1) / kSmallKC;
+    if (tiles >= 256 || nchunk <= 4) return 4;
+    return nchunk <= 8 ? 8 : 16;
+}
+
+int64_t small_tiles(const GemmArgs &g) { return (int64_t)((g.M + 31) / 32) * ((g.N + 31) / 32) * g.batch; }
 
 struct TileCfg {
     int bm, bn, wgm;
@@ -929,11 +952,12 @@ GemmPlan plan_auto(int M, int N, int K, int batch, bool im2col) {
     // Few output tiles and a small operand footprint: the small-GEMM kernel
     // (32x32 tiles, K split over the block's waves, no split-K pass).  Its
     // L2 traffic grows with the tile count (each operand is re-read once per
-    // 32-wide strip of the other), hence the footprint bound.
+    // 32-wide strip of the other), hence the footprint bound.  Bounds from a
+    // network sweep (200/40, 400/80, 700/160 tiles/MB): 400/80 was fastest.
     const int64_t t64 = (int64_t)((M + 63) / 64) * ((N + 63) / 64) * batch;
     const int64_t reread = 4 * ((int64_t)M * K * ((N + 31) / 32) + (int64_t)K * N * ((M + 31) / 32)) * batch;
-    static const int64_t small_t64 = env_int("PPDL_SMALL_T64", 200);
-    static const int64_t small_mb = env_int("PPDL_SMALL_MB", 40);
+    static const int64_t small_t64 = env_int("PPDL_SMALL_T64", 400);
+    static const int64_t small_mb = env_int("PPDL_SMALL_MB", 80);
     if (!im2col && t64 < small_t64 && reread <= (small_mb << 20)) return GemmPlan{kCfgSmall, 1};
     GemmPlan p{M <= 32 ? 5 : 3, 1};
     const int nk = (K + kBK - 1) / kBK;
@@ -1050,8 +1074,11 @@ hipError_t launch_small(const GemmArgs &g, hipStream_t s) {
     const int64_t a_ext = AMODE == 0 ? (int64_t)g.K * g.lda : (int64_t)g.M * g.lda;
     if (total <= 0 || total > 0x7fffffff || a_ext > 0x7fffffff || (int64_t)g.K * g.ldb > 0x7fffffff)
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_gemm_small<AMODE>, dim3((unsigned)total), dim3(kThreads), 0, s, g, tiles_m,
-                       tiles_m * tiles_n);
+    const dim3 grid((unsigned)total);
+    const int wv = small_waves(g.K, total);
+    if (wv == 4) hipLaunchKernelGGL((k_gemm_small<AMODE, 4>), grid, dim3(256), 0, s, g, tiles_m, tiles_m * tiles_n);
+    else if (wv == 8) hipLaunchKernelGGL((k_gemm_small<AMODE, 8>), grid, dim3(512), 0, s, g, tiles_m, tiles_m * tiles_n);
+    else hipLaunchKernelGGL((k_gemm_small<AMODE, 16>), grid, dim3(1024), 0, s, g, tiles_m, tiles_m * tiles_n);
     return hipGetLastError();
 }
 
@@ -1119,7 +1146,8 @@ hipError_t gemm_dense(const GemmArgs &g, const GemmWorkspace &ws, hipStream_t s)
 std::string gemm_kernel_name(const GemmArgs &g, int64_t ws_bytes, bool im2col) {
     if (im2col && patch_cc(g)) return g.KW == 3 ? "k_conv_patch<3, 2>" : "k_conv_patch<2, 1>";
     const GemmPlan p = gemm_plan(g, ws_bytes, im2col);
-    if (p.cfg == kCfgSmall) return g.a_rowmajor ? "k_gemm_small<1>" : "k_gemm_small<0>";
+    if (p.cfg == kCfgSmall)
+        return std::string("k_gemm_small<") + (g.a_rowmajor ? "1, " : "0, ") + std::to_string(small_waves(g.K, small_tiles(g))) + ">";
     int bm = kCfgs[p.cfg].bm, bn = kCfgs[p.cfg].bn, wgm = kCfgs[p.cfg].wgm;
     if (g.a_rowmajor && p.cfg != 5) bm = 64, bn = 64, wgm = 2;  // the two row-major-A shapes
     char buf[96];
