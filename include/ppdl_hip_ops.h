@@ -83,7 +83,8 @@ PPDL_HIP_API int ppdl_hip_supports(const int32_t op_params[16], const ppdl_tview
  *
  * Per-op contract (srcs in order, all F32 contiguous unless stated):
  *  2  MSDEF     src: value ne(256,13125), offsets ne(192,NQ), attn logits
- *               ne(96,NQ), ref cxcywh ne(4,NQ); dst ne(256,NQ).
+ *               ne(96,NQ), ref cxcywh ne(4,NQ); dst ne(256,NQ).  value,
+ *               offsets and logits may be row-strided (nb[1] >= 4*ne[0]).
  *  3  CONV      src: x ne(W,H,IC), wr ne(OC,IC,1), bias ne(OC) (unused);
  *               params[14] = K | pad<<8 with K=1, pad=0; params[15] = 0
  *               (CHW out); dst ne(W,H,OC) = sum_ic x*wr, no bias.

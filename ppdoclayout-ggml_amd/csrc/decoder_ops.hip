@@ -24,18 +24,21 @@ __constant__ int kLvlStart[3] = {0, 10000, 12500};
 // so every gather is one 128-byte segment.
 //   val  (13125, 256) token-major       off (NQ, 192) [((h*3+l)*4+p)*2+xy]
 //   awr  (NQ, 96) pre-softmax [h*12 + l*4 + p]   ref (NQ, 4) cxcywh
+// val, off and awr rows may be strided (ldv, ldo, ldw floats): slices of a
+// wider projection.
 __global__ __launch_bounds__(256) void k_msdeform(const float *__restrict__ val,
                                                   const float *__restrict__ off,
                                                   const float *__restrict__ awr,
                                                   const float *__restrict__ ref,
-                                                  float *__restrict__ out, int nq, int ldv) {
+                                                  float *__restrict__ out, int nq, int ldv, int ldo,
+                                                  int ldw) {
     const int q = blockIdx.x;
     if (q >= nq) return;
     const int h = threadIdx.x >> 5, c = threadIdx.x & 31;
     const float rx = ref[q * 4 + 0], ry = ref[q * 4 + 1];
     const float rw = ref[q * 4 + 2], rh = ref[q * 4 + 3];
 
-    const float *a = awr + (int64_t)q * 96 + h * 12;
+    const float *a = awr + (int64_t)q * ldw + h * 12;
     float w[12];
     float amax = a[0];
 #pragma unroll
@@ -49,7 +52,7 @@ __global__ __launch_bounds__(256) void k_msdeform(const float *__restrict__ val,
 #pragma unroll
     for (int i = 0; i < 12; i++) w[i] /= wsum;
 
-    const float *o = off + (int64_t)q * 192 + h * 24;
+    const float *o = off + (int64_t)q * ldo + h * 24;
     const float *vh = val + h * kHD + c;
     // Corner tokens and weights first, the 48 gathers next (all issued
     // together), the accumulation last in the reference's l -> p -> corner
@@ -309,9 +312,9 @@ __global__ __launch_bounds__(kTopkThreads) void k_topk(const float *__restrict__
 
 }  // namespace
 
-hipError_t msdeform(const float *val, int ldv, const float *off, const float *awr, const float *ref,
-                    float *out, int nq, hipStream_t s) {
-    hipLaunchKernelGGL(k_msdeform, dim3(nq), dim3(256), 0, s, val, off, awr, ref, out, nq, ldv);
+hipError_t msdeform(const float *val, int ldv, const float *off, int ldo, const float *awr, int ldw,
+                    const float *ref, float *out, int nq, hipStream_t s) {
+    hipLaunchKernelGGL(k_msdeform, dim3(nq), dim3(256), 0, s, val, off, awr, ref, out, nq, ldv, ldo, ldw);
     return hipGetLastError();
 }
 

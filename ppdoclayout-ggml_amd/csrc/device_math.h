@@ -1,0 +1,33 @@
+// Device-side scalar helpers shared by the kernels: the activation codes of
+// the GEMM / elementwise epilogues and the box-refinement inverse sigmoid.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include "ppdl_internal.h"
+
+namespace ppdl {
+
+// 0 none, 1 ReLU, 2 SiLU, 3 GELU (erf form), 4 sigmoid: ggml's relu / silu /
+// gelu_erf / sigmoid
+__device__ __forceinline__ float act_f(float v, int act) {
+    if (act == kActRelu) return v > 0.0f ? v : 0.0f;
+    if (act == kActSilu) return v / (1.0f + expf(-v));
+    if (act == kActGelu) return 0.5f * v * (1.0f + erff(v * 0.70710678118654752f));
+    if (act == kActSigmoid) return 1.0f / (1.0f + expf(-v));
+    return v;
+}
+
+// src/ppdoclayout.cpp:589-594: clamp to [0,1], log(max(x,1e-5)) - log(max(1-x,1e-5))
+__device__ __forceinline__ float inv_sigmoid(float x) {
+    x = fminf(fmaxf(x, 0.0f), 1.0f);
+    const float x1 = fminf(fmaxf(x, 1e-5f), 1.0f);
+    const float x2 = fminf(fmaxf(1.0f - x, 1e-5f), 1.0f);
+    return logf(x1) - logf(x2);
+}
+
+// box refinement (src/ppdoclayout.cpp:860-862): sigmoid(delta + inv_sigmoid(ref))
+__device__ __forceinline__ float refine_box(float delta, float ref) {
+    return 1.0f / (1.0f + expf(-(delta + inv_sigmoid(ref))));
+}
+
+}  // namespace ppdl

@@ -1,16 +1,10 @@
 // Bandwidth kernels: op 5 bias+act and the F32 im2col in ggml's layout.
 #include <algorithm>
 
-#include "ppdl_internal.h"
+#include "device_math.h"
 
 namespace ppdl {
 namespace {
-
-__device__ __forceinline__ float act_f(float v, int act) {
-    if (act == 1) return v > 0.0f ? v : 0.0f;
-    if (act == 2) return v / (1.0f + expf(-v));
-    return v;
-}
 
 // out[i] = act(in[i] + bias[i / plane])   (patches/ggml-ppdl.patch:417-432)
 // Vector path: 4 consecutive elements share one bias when plane % 4 == 0.

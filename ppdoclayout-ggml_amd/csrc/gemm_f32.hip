@@ -35,7 +35,7 @@
 #include <cstdlib>
 #include <type_traits>
 
-#include "ppdl_internal.h"
+#include "device_math.h"
 
 namespace ppdl {
 namespace {
@@ -44,16 +44,6 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kThreads = 256;
 constexpr int kBK = 32;
-
-// 0 none, 1 ReLU, 2 SiLU, 3 GELU (erf form), 4 sigmoid — ggml's relu /
-// silu / gelu_erf / sigmoid
-__device__ __forceinline__ float act_f(float v, int act) {
-    if (act == 1) return v > 0.0f ? v : 0.0f;
-    if (act == 2) return v / (1.0f + expf(-v));
-    if (act == 3) return 0.5f * v * (1.0f + erff(v * 0.70710678118654752f));
-    if (act == 4) return 1.0f / (1.0f + expf(-v));
-    return v;
-}
 
 // Blocks are dispatched round-robin over the 8 XCDs (hardware id % 8).  Give
 // each XCD a contiguous range of logical tiles so that tiles sharing operands
@@ -120,6 +110,7 @@ __device__ __forceinline__ void gemm_epilogue(const f32x16 (&acc)[TM][TN], const
         if (add_mode == 1) v += Ad[idx];
         v = act_f(v, act);
         if (add_mode == 2) v += Ad[idx];
+        else if (add_mode == 3) v = refine_box(v, Ad[idx]);
         return v;
     };
     if (!g.c_trans) {
@@ -776,6 +767,7 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(const float *__restrict__
         if (g.add_mode == 1) x += Ad[idx];
         x = act_f(x, g.act);
         if (g.add_mode == 2) x += Ad[idx];
+        else if (g.add_mode == 3) x = refine_box(x, Ad[idx]);
         C[idx] = x;
     }
 }
@@ -797,7 +789,7 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(const float *__restrict__
 // (AMODE 1) is then one float4 per lane per c.
 constexpr int kSmallKC = 32;
 
-template <int AMODE, int WV>
+template <int AMODE, int WV, bool PRE>
 __global__ __launch_bounds__(WV * 64) void k_gemm_small(GemmArgs g, int tiles_m, int tiles_mn) {
     constexpr int KC = kSmallKC, NS = KC / 2, NT = WV * 64;
     __shared__ float red[WV][32][33];
@@ -811,6 +803,11 @@ __global__ __launch_bounds__(WV * 64) void k_gemm_small(GemmArgs g, int tiles_m,
     const int lda = (int)g.lda, ldb = (int)g.ldb;
     const float *__restrict__ A = g.A + (int64_t)bz * g.sA;
     const float *__restrict__ B = g.B + (int64_t)bz * g.sB;
+    // prologue add (PRE, row-major A): a_add has A's layout; tiles at or past
+    // column a_add_n load it too and select zero (no branch between the
+    // loads, which would make the compiler wait for each one)
+    const float *__restrict__ A2 = PRE ? g.a_add + (int64_t)bz * g.sA : nullptr;
+    const bool pre = PRE && n0 < g.a_add_n;
     const int mc = min(m0 + l32, M - 1), nc = min(n0 + l32, N - 1);
     const int nchunk = (K + KC - 1) / KC;
 
@@ -821,7 +818,15 @@ __global__ __launch_bounds__(WV * 64) void k_gemm_small(GemmArgs g, int tiles_m,
             const int k4 = kb + 8 * c + 4 * h;  // this lane's 4 consecutive k
             if (AMODE == 1) {
                 // K % 4 == 0: the 4 k are all inside or all outside
-                const float4 v = ld4(A + (uint32_t)(mc * lda + min(k4, K - 4)));
+                const uint32_t ai = (uint32_t)(mc * lda + min(k4, K - 4));
+                float4 v = ld4(A + ai);
+                if (PRE) {
+                    const float4 p = ld4(A2 + ai);
+                    v.x += pre ? p.x : 0.0f;
+                    v.y += pre ? p.y : 0.0f;
+                    v.z += pre ? p.z : 0.0f;
+                    v.w += pre ? p.w : 0.0f;
+                }
                 const bool in = k4 < K;
                 a[4 * c + 0] = in ? v.x : 0.0f;
                 a[4 * c + 1] = in ? v.y : 0.0f;
@@ -892,6 +897,7 @@ __global__ __launch_bounds__(WV * 64) void k_gemm_small(GemmArgs g, int tiles_m,
             if (g.add_mode == 1) v += Ad[idx];
             v = act_f(v, g.act);
             if (g.add_mode == 2) v += Ad[idx];
+            else if (g.add_mode == 3) v = refine_box(v, Ad[idx]);
             C[idx] = v;
         }
     }
@@ -1067,6 +1073,14 @@ hipError_t launch(const GemmArgs &g, int S, const GemmWorkspace &ws, hipStream_t
     return hipGetLastError();
 }
 
+template <int AMODE, bool PRE>
+hipError_t launch_small_wv(const GemmArgs &g, int wv, dim3 grid, int tiles_m, int tmn, hipStream_t s) {
+    if (wv == 4) hipLaunchKernelGGL((k_gemm_small<AMODE, 4, PRE>), grid, dim3(256), 0, s, g, tiles_m, tmn);
+    else if (wv == 8) hipLaunchKernelGGL((k_gemm_small<AMODE, 8, PRE>), grid, dim3(512), 0, s, g, tiles_m, tmn);
+    else hipLaunchKernelGGL((k_gemm_small<AMODE, 16, PRE>), grid, dim3(1024), 0, s, g, tiles_m, tmn);
+    return hipGetLastError();
+}
+
 template <int AMODE>
 hipError_t launch_small(const GemmArgs &g, hipStream_t s) {
     const int tiles_m = (g.M + 31) / 32, tiles_n = (g.N + 31) / 32;
@@ -1075,11 +1089,10 @@ hipError_t launch_small(const GemmArgs &g, hipStream_t s) {
     if (total <= 0 || total > 0x7fffffff || a_ext > 0x7fffffff || (int64_t)g.K * g.ldb > 0x7fffffff)
         return hipErrorInvalidValue;
     const dim3 grid((unsigned)total);
-    const int wv = small_waves(g.K, total);
-    if (wv == 4) hipLaunchKernelGGL((k_gemm_small<AMODE, 4>), grid, dim3(256), 0, s, g, tiles_m, tiles_m * tiles_n);
-    else if (wv == 8) hipLaunchKernelGGL((k_gemm_small<AMODE, 8>), grid, dim3(512), 0, s, g, tiles_m, tiles_m * tiles_n);
-    else hipLaunchKernelGGL((k_gemm_small<AMODE, 16>), grid, dim3(1024), 0, s, g, tiles_m, tiles_m * tiles_n);
-    return hipGetLastError();
+    const int wv = small_waves(g.K, total), tmn = tiles_m * tiles_n;
+    if constexpr (AMODE == 1)
+        if (g.a_add) return launch_small_wv<AMODE, true>(g, wv, grid, tiles_m, tmn, s);
+    return launch_small_wv<AMODE, false>(g, wv, grid, tiles_m, tmn, s);
 }
 
 template <int BMODE>
@@ -1089,6 +1102,8 @@ hipError_t dispatch(const GemmArgs &g_in, const GemmWorkspace &ws, hipStream_t s
     if (BMODE == 1)
         if (const int cc = patch_cc(g)) return launch_patch(g, cc, s);
     const GemmPlan p = gemm_plan(g, ws.bytes, BMODE == 1);
+    if (g.a_add && (BMODE != 0 || !g.a_rowmajor || (((uintptr_t)g.a_add) & 15) != 0 || g.a_add_n % 32 != 0))
+        return hipErrorInvalidValue;
     if (BMODE == 0 && p.cfg == kCfgSmall) {
         if (g.a_rowmajor && (g.K % 4 != 0 || g.lda % 4 != 0 || (((uintptr_t)g.A) & 15) != 0))
             return hipErrorInvalidValue;
@@ -1131,6 +1146,8 @@ GemmPlan gemm_plan(const GemmArgs &g, int64_t ws_bytes, bool im2col) {
     } else {
         best = plan_auto(g.M, g.N, g.K, g.batch, im2col);
     }
+    // the prologue add exists in the small kernel only
+    if (g.a_add && !im2col) best = GemmPlan{kCfgSmall, 1};
     // never plan more splits than the workspace holds
     while (best.splits > 1 && gemm_ws_bytes(g.M, g.N, g.batch, best.cfg, best.splits) > ws_bytes) best.splits--;
     return best;
@@ -1147,7 +1164,8 @@ std::string gemm_kernel_name(const GemmArgs &g, int64_t ws_bytes, bool im2col) {
     if (im2col && patch_cc(g)) return g.KW == 3 ? "k_conv_patch<3, 2>" : "k_conv_patch<2, 1>";
     const GemmPlan p = gemm_plan(g, ws_bytes, im2col);
     if (p.cfg == kCfgSmall)
-        return std::string("k_gemm_small<") + (g.a_rowmajor ? "1, " : "0, ") + std::to_string(small_waves(g.K, small_tiles(g))) + ">";
+        return std::string("k_gemm_small<") + (g.a_rowmajor ? "1, " : "0, ") +
+               std::to_string(small_waves(g.K, small_tiles(g))) + (g.a_add && g.a_rowmajor ? ", true>" : ", false>");
     int bm = kCfgs[p.cfg].bm, bn = kCfgs[p.cfg].bn, wgm = kCfgs[p.cfg].wgm;
     if (g.a_rowmajor && p.cfg != 5) bm = 64, bn = 64, wgm = 2;  // the two row-major-A shapes
     char buf[96];

@@ -95,6 +95,15 @@ ppdl_tview planes(const float *d, int64_t T, int64_t C, int64_t ldt) {
     return v;
 }
 
+// ne(cols, rows) rows of `cols` floats, `ld` floats apart (a column slice of
+// a wider row-major matrix)
+ppdl_tview row_view(const float *d, int64_t cols, int64_t rows, int64_t ld) {
+    ppdl_tview v = view(d, {cols, rows});
+    v.nb[1] = ld * 4;
+    v.nb[2] = v.nb[3] = v.nb[1] * rows;
+    return v;
+}
+
 std::vector<int32_t> op_params(int op, int p14, int p15) {
     std::vector<int32_t> v(16, 0);
     v[12] = (int32_t)PPDL_MAGIC;
@@ -119,6 +128,8 @@ class Net {
     }
 
     bool load(const std::string &path, std::string *err);
+    bool concat_linears(GgufFile &g, const std::vector<std::string> &parts, const std::string &name,
+                        std::string *err);
     bool build(bool dumps, std::string *err);
     bool capture(std::string *err);
     int replay();  // one graph launch + sync
@@ -257,10 +268,10 @@ class Net {
     Img conv(const Img &x, const std::string &name, int s, int p, int act, float *out = nullptr, int pad_end = 0,
              const float *add = nullptr, int add_mode = 0);
     Seq lin(const Seq &x, const std::string &name, int act, float *out = nullptr, const float *add = nullptr,
-            int add_mode = 0);
+            int add_mode = 0, const float *a_add = nullptr, int a_add_n = 0);
     Seq ln(const Seq &a, const float *b, const std::string &name, float *out = nullptr, int out_chw = 0);
     Seq mlp3(const Seq &x, const std::string &pfx);
-    Seq mha(const Seq &qk_in, const Seq &v_in, const std::string &pfx, float *out, const float *resid);
+    Seq mha(const Seq &x, const float *pos, const std::string &pfx, float *out, const float *resid);
     void hg_block(const Img &cat, int cin, const std::string &pfx, bool light, int mid, Img *y, float *out,
                   const float *resid);
     Img csp(const Img &x, const std::string &pfx, float *out);
@@ -298,8 +309,8 @@ class Net {
 // Loading: read every tensor, repack conv weights (.wr [tap][ic][oc] and, for
 // 3x3, the 36-plane .wg4), store linear weights transposed (.wt [in][out])
 // for the row-major-activation GEMM, keep biases / norms / depthwise weights
-// as they are.  The self-attention q and k projections share their input, so
-// they are also stored side by side (".qk").
+// as they are.  Linears that share their input are also stored side by side
+// (concat_linears).
 bool Net::load(const std::string &path, std::string *err) {
     GgufFile g;
     if (!gguf_open(path, &g, err)) return false;
@@ -333,72 +344,58 @@ bool Net::load(const std::string &path, std::string *err) {
             return false;
         }
     }
-    // fused q|k projections
-    std::vector<std::string> att = {"aifi"};
-    for (int i = 0; i < 6; i++) att.push_back("dec" + std::to_string(i) + ".sa");
-    for (const auto &a : att) {
-        if (!g.index.count(a + ".q.weight") || !g.index.count(a + ".k.weight")) continue;
-        const auto &tq = g.tensors[g.index[a + ".q.weight"]];
-        const int64_t in = tq.ne[0], out = tq.ne[1];
-        std::vector<float> q((size_t)(in * out)), k(q.size()), qb((size_t)out), kb((size_t)out);
-        if (!gguf_read_f32(g, tq, q.data(), err) ||
-            !gguf_read_f32(g, g.tensors[g.index[a + ".k.weight"]], k.data(), err) ||
-            !gguf_read_f32(g, g.tensors[g.index[a + ".q.bias"]], qb.data(), err) ||
-            !gguf_read_f32(g, g.tensors[g.index[a + ".k.bias"]], kb.data(), err))
-            return false;
-        std::vector<float> wt((size_t)(in * 2 * out)), b((size_t)(2 * out));
-        for (int64_t o = 0; o < out; o++) {
-            for (int64_t i = 0; i < in; i++) {
-                wt[(size_t)(i * 2 * out + o)] = q[(size_t)(o * in + i)];
-                wt[(size_t)(i * 2 * out + out + o)] = k[(size_t)(o * in + i)];
-            }
-            b[(size_t)o] = qb[(size_t)o];
-            b[(size_t)(out + o)] = kb[(size_t)o];
-        }
-        w_[a + ".qk.wt"] = upload(wt);
-        w_[a + ".qk.bias"] = upload(b);
-        ne_[a + ".qk.weight"] = {in, 2 * out};
+    // Linears that read the same input run as one GEMM over their weights
+    // stored side by side: q|k|v of each attention, the decoder's sampling
+    // offsets | attention logits, and the six decoder layers' value
+    // projections of the encoder tokens.
+    for (const std::string a : {"aifi", "dec0.sa", "dec1.sa", "dec2.sa", "dec3.sa", "dec4.sa", "dec5.sa"})
+        if (!concat_linears(g, {a + ".q", a + ".k", a + ".v"}, a + ".qkv", err)) return false;
+    for (int i = 0; i < 6; i++) {
+        const std::string d = "dec" + std::to_string(i) + ".ca";
+        if (!concat_linears(g, {d + ".so", d + ".aw"}, d + ".soaw", err)) return false;
     }
-    // the six decoder layers' value projections read the same encoder
-    // tokens: one [256][6*256] weight, so they run as one GEMM
     {
-        std::vector<float> wt, b;
-        int64_t in = 0, out = 0;
-        bool all = true;
-        for (int i = 0; i < 6 && all; i++) {
-            const std::string a = "dec" + std::to_string(i) + ".ca.vp";
-            if (!g.index.count(a + ".weight") || !g.index.count(a + ".bias")) {
-                all = false;
-                break;
-            }
-            const auto &tw = g.tensors[g.index[a + ".weight"]];
-            if (i == 0) {
-                in = tw.ne[0];
-                out = tw.ne[1];
-                wt.assign((size_t)(in * 6 * out), 0.0f);
-                b.assign((size_t)(6 * out), 0.0f);
-            } else if (tw.ne[0] != in || tw.ne[1] != out) {
-                all = false;
-                break;
-            }
-            std::vector<float> h((size_t)(in * out)), hb((size_t)out);
-            if (!gguf_read_f32(g, tw, h.data(), err) || !gguf_read_f32(g, g.tensors[g.index[a + ".bias"]], hb.data(), err))
-                return false;
-            for (int64_t o = 0; o < out; o++) {
-                for (int64_t k = 0; k < in; k++) wt[(size_t)(k * 6 * out + i * out + o)] = h[(size_t)(o * in + k)];
-                b[(size_t)(i * out + o)] = hb[(size_t)o];
-            }
-        }
-        if (all && out > 0) {
-            w_["dec.ca.vp.wt"] = upload(wt);
-            w_["dec.ca.vp.bias"] = upload(b);
-            ne_["dec.ca.vp.weight"] = {in, 6 * out};
-        }
+        std::vector<std::string> vp;
+        for (int i = 0; i < 6; i++) vp.push_back("dec" + std::to_string(i) + ".ca.vp");
+        if (!concat_linears(g, vp, "dec.ca.vp", err)) return false;
     }
     if (oom_) {
         *err = "device allocation failed";
         return false;
     }
+    return true;
+}
+
+// Linears `parts` (weights ne(in, out_i), biases ne(out_i)) stored as one
+// transposed weight [in][sum out_i] and one bias under `name`.  Skipped (no
+// entry; the graph build then reports the missing weight) when a part is
+// absent or the input widths differ.
+bool Net::concat_linears(GgufFile &g, const std::vector<std::string> &parts, const std::string &name,
+                         std::string *err) {
+    int64_t in = -1, total = 0;
+    for (const auto &p : parts) {
+        if (!g.index.count(p + ".weight") || !g.index.count(p + ".bias")) return true;
+        const auto &t = g.tensors[g.index[p + ".weight"]];
+        if (t.ne.size() != 2 || (in >= 0 && t.ne[0] != in)) return true;
+        if (g.tensors[g.index[p + ".bias"]].nelem() != t.ne[1]) return true;
+        in = t.ne[0];
+        total += t.ne[1];
+    }
+    std::vector<float> wt((size_t)(in * total)), b((size_t)total), h;
+    int64_t o0 = 0;
+    for (const auto &p : parts) {
+        const auto &t = g.tensors[g.index[p + ".weight"]];
+        const int64_t out = t.ne[1];
+        h.resize((size_t)(in * out));
+        if (!gguf_read_f32(g, t, h.data(), err) || !gguf_read_f32(g, g.tensors[g.index[p + ".bias"]], b.data() + o0, err))
+            return false;
+        for (int64_t o = 0; o < out; o++)
+            for (int64_t i = 0; i < in; i++) wt[(size_t)(i * total + o0 + o)] = h[(size_t)(o * in + i)];
+        o0 += out;
+    }
+    w_[name + ".wt"] = upload(wt);
+    w_[name + ".bias"] = upload(b);
+    ne_[name + ".weight"] = {in, total};
     return true;
 }
 
@@ -476,8 +473,10 @@ Img Net::conv(const Img &x, const std::string &name, int s, int p, int act, floa
 }
 
 // lin (:545-548): y = x W^T + b as a row-major-activation GEMM; optional act
-// and fused add (residual) in the epilogue.
-Seq Net::lin(const Seq &x, const std::string &name, int act, float *out, const float *add, int add_mode) {
+// and fused add (residual) in the epilogue, and an optional prologue add
+// (x + a_add, same layout as x) for output columns < a_add_n.
+Seq Net::lin(const Seq &x, const std::string &name, int act, float *out, const float *add, int add_mode,
+             const float *a_add, int a_add_n) {
     const auto &ne = shape(name + ".weight");  // (in, out)
     const int in = (int)ne[0], nout = (int)ne[1];
     if (in != x.D && bad_node_.empty()) bad_node_ = name + " (feature mismatch)";
@@ -499,6 +498,8 @@ Seq Net::lin(const Seq &x, const std::string &name, int act, float *out, const f
     g.act = act;
     g.add = add;
     g.add_mode = add_mode;
+    g.a_add = a_add;
+    g.a_add_n = a_add_n;
     gemm(name, g);
     return y;
 }
@@ -518,14 +519,15 @@ Seq Net::mlp3(const Seq &x, const std::string &pfx) {
     return lin(h, pfx + ".2", kActNone);
 }
 
-// mha (:572-587) + output projection; out = x_resid + o(attn) when resid given
-Seq Net::mha(const Seq &qk_in, const Seq &v_in, const std::string &pfx, float *out, const float *resid) {
-    const int T = qk_in.T;
-    Seq qk = lin(qk_in, pfx + ".qk", kActNone);  // [T][512]: q | k
-    Seq v = lin(v_in, pfx + ".v", kActNone);
+// mha (:572-587) + output projection: q, k from x + pos, v from x, as one
+// GEMM [T][768] = q | k | v whose prologue adds pos for the q|k columns;
+// out = resid + o(attn) when resid given
+Seq Net::mha(const Seq &x, const float *pos, const std::string &pfx, float *out, const float *resid) {
+    const int T = x.T;
+    Seq qkv = lin(x, pfx + ".qkv", kActNone, nullptr, nullptr, 0, pos, 2 * kDM);
     Seq att{alloc((int64_t)T * kDM), T, kDM, kDM};
     node(pfx + ".attn", 1, [=](hipStream_t st) {
-        return ok(attention(qk.d, 2 * kDM, qk.d + kDM, 2 * kDM, v.d, kDM, att.d, kDM, T, st));
+        return ok(attention(qkv.d, 3 * kDM, qkv.d + kDM, 3 * kDM, qkv.d + 2 * kDM, 3 * kDM, att.d, kDM, T, st));
     });
     return lin(att, pfx + ".o", kActNone, out, resid, resid ? 2 : 0);
 }
@@ -624,13 +626,11 @@ bool Net::build(bool dumps, std::string *err) {
     conv(s2, "enc_in1", 1, 0, kActNone, cat16.d + 256LL * 2500);  // p16 -> fpn0 concat slice 1
     Img p32 = conv(s3, "enc_in2", 1, 0, kActNone);                 // 25, 256
     {
-        // AIFI (:683-696): to_seq, qk = s + pos, post-norm MHA and FFN
+        // AIFI (:683-696): to_seq, q = k = s + pos (in the q|k|v GEMM), post-norm MHA and FFN
         Seq s{alloc(625LL * kDM), 625, kDM, kDM};
         const Img pi = p32;
         node("aifi.to_seq", 1, [=](hipStream_t st) { return ok(transpose(pi.d, s.d, kDM, 625, kDM, st)); });
-        Seq qk{alloc(625LL * kDM), 625, kDM, kDM};
-        node("aifi.pos", 1, [=](hipStream_t st) { return ok(add(s.d, pos_, qk.d, 625LL * kDM, st)); });
-        Seq at = mha(qk, s, "aifi", nullptr, nullptr);
+        Seq at = mha(s, pos_, "aifi", nullptr, nullptr);
         Seq s1n = ln(at, s.d, "aifi.ln1");
         Seq ff = lin(lin(s1n, "aifi.fc1", kActGelu), "aifi.fc2", kActNone);
         Seq back = ln(ff, s1n.d, "aifi.ln2", nullptr, 1);  // channel-major == (25,25,256) image
@@ -701,13 +701,9 @@ bool Net::build(bool dumps, std::string *err) {
     dump("source", source.d, {kDM, NTOK});
     // value projections of all six decoder layers at once (layer i: columns
     // 256i..256i+255), on lane 2 until the first deformable attention
-    const bool vp_cat = w_.count("dec.ca.vp.wt") != 0;
-    Seq vcat{};
-    if (vp_cat) {
-        fork(2);
-        vcat = lin(source, "dec.ca.vp", kActNone);
-        main_lane();
-    }
+    fork(2);
+    const Seq vcat = lin(source, "dec.ca.vp", kActNone);
+    main_lane();
     Seq memory{alloc((int64_t)NTOK * kDM), NTOK, kDM, kDM};
     node("memory", 1, [=](hipStream_t st) { return ok(mul_rows(source.d, valid_, memory.d, NTOK, kDM, st)); });
     Seq om = ln(lin(memory, "enc_out.l", kActNone), nullptr, "enc_out.ln");
@@ -756,36 +752,25 @@ bool Net::build(bool dumps, std::string *err) {
     for (int i = 0; i < 6; i++) {
         const std::string dp = "dec" + std::to_string(i);
         Seq qpos = lin(lin(ref, "qpos.0", kActRelu), "qpos.1", kActNone);
-        Seq qk{alloc((int64_t)NQ * kDM), NQ, kDM, kDM};
-        const Seq xi = xq;
-        node(dp + ".qk", 1, [=](hipStream_t st) { return ok(add(xi.d, qpos.d, qk.d, (int64_t)NQ * kDM, st)); });
-        Seq sa = mha(qk, xq, dp + ".sa", nullptr, xq.d);  // x + attn
+        Seq sa = mha(xq, qpos.d, dp + ".sa", nullptr, xq.d);  // x + attn, q = k = x + qpos
         xq = ln(sa, nullptr, dp + ".ln1");
-        Seq z{alloc((int64_t)NQ * kDM), NQ, kDM, kDM};
-        const Seq x1 = xq;
-        node(dp + ".z", 1, [=](hipStream_t st) { return ok(add(x1.d, qpos.d, z.d, (int64_t)NQ * kDM, st)); });
-        ppdl_tview vval;
-        if (vp_cat && i == 0) join(2);
-        if (vp_cat) {
-            vval = view(vcat.d + (int64_t)i * kDM, {kDM, NTOK});  // row stride 6*256
-            vval.nb[1] = (int64_t)vcat.ld * 4;
-            vval.nb[2] = vval.nb[3] = vval.nb[1] * NTOK;
-        } else {
-            vval = view(lin(source, dp + ".ca.vp", kActNone).d, {kDM, NTOK});
-        }
-        Seq offs = lin(z, dp + ".ca.so", kActNone);
-        Seq aw = lin(z, dp + ".ca.aw", kActNone);
+        if (i == 0) join(2);
+        // sampling offsets | attention logits of (x + qpos), one [NQ][288] GEMM
+        Seq soaw = lin(xq, dp + ".ca.soaw", kActNone, nullptr, nullptr, 0, qpos.d, 1 << 30);
         Seq ca{alloc((int64_t)NQ * kDM), NQ, kDM, kDM};
         tagged(dp + ".msdeform", PPDL_OP_MSDEF, 0, 0, view(ca.d, {kDM, NQ}),
-               {vval, view(offs.d, {192, NQ}), view(aw.d, {96, NQ}), view(ref.d, {4, NQ})});
+               {row_view(vcat.d + (int64_t)i * kDM, kDM, NTOK, vcat.ld), row_view(soaw.d, 192, NQ, soaw.ld),
+                row_view(soaw.d + 192, 96, NQ, soaw.ld), view(ref.d, {4, NQ})});
         Seq cao = lin(ca, dp + ".ca.op", kActNone, nullptr, xq.d, 2);  // x + ca
         xq = ln(cao, nullptr, dp + ".ln2");
         Seq ff = lin(lin(xq, dp + ".fc1", kActRelu), dp + ".fc2", kActNone, nullptr, xq.d, 2);
         xq = ln(ff, nullptr, dp + ".ln3");
         static const char *hn[6] = {"hidden0", "hidden1", "hidden2", "hidden3", "hidden4", "hidden5"};
         dump(hn[i], xq.d, {kDM, NQ});
-        Seq delta = mlp3(xq, "bbox_head");
-        node(dp + ".ref", 1, [=](hipStream_t st) { return ok(box_update(delta.d, boxes_, NQ * 4, st)); });
+        // box refinement ref = sigmoid(delta + inv_sigmoid(ref)) in the last
+        // bbox-head GEMM's epilogue, in place
+        Seq bh = lin(lin(xq, "bbox_head.0", kActRelu), "bbox_head.1", kActRelu);
+        lin(bh, "bbox_head.2", kActNone, boxes_, boxes_, 3);
     }
 
     // ---- heads (:865-876)

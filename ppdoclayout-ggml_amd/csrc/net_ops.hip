@@ -5,20 +5,13 @@
 // (src/ppdoclayout.cpp:363-883); each kernel cites its call site.
 #include <algorithm>
 
+#include "device_math.h"
 #include "net_internal.h"
 
 #pragma clang fp contract(off)
 
 namespace ppdl {
 namespace {
-
-__device__ __forceinline__ float act_f(float v, int act) {
-    if (act == kActRelu) return v > 0.0f ? v : 0.0f;
-    if (act == kActSilu) return v / (1.0f + expf(-v));
-    if (act == kActGelu) return 0.5f * v * (1.0f + erff(v * 0.70710678118654752f));
-    if (act == kActSigmoid) return 1.0f / (1.0f + expf(-v));
-    return v;
-}
 
 // ---------------------------------------------------------------------------
 // Depthwise conv + bias + act (ggml_conv_2d_dw_direct + add + act,
@@ -314,22 +307,13 @@ __global__ __launch_bounds__(256) void k_mul_rows(const float *__restrict__ x, c
     if (i < T * D) out[i] = x[i] * mask[i / D];
 }
 
-__device__ __forceinline__ float inv_sigmoid(float x) {
-    // src/ppdoclayout.cpp:589-594: clamp to [0,1], log(max(x,1e-5)) - log(max(1-x,1e-5))
-    x = fminf(fmaxf(x, 0.0f), 1.0f);
-    const float x1 = fminf(fmaxf(x, 1e-5f), 1.0f);
-    const float x2 = fminf(fmaxf(1.0f - x, 1e-5f), 1.0f);
-    return logf(x1) - logf(x2);
-}
-
 // Box refinement (src/ppdoclayout.cpp:860-862): ref = sigmoid(delta + inv_sigmoid(ref)).
 // With delta == null: ref = sigmoid(ref) (the initial reference).
 __global__ __launch_bounds__(256) void k_box_update(const float *__restrict__ delta, float *__restrict__ ref,
                                                     int n) {
     const int i = blockIdx.x * 256 + threadIdx.x;
     if (i >= n) return;
-    const float z = delta ? delta[i] + inv_sigmoid(ref[i]) : ref[i];
-    ref[i] = 1.0f / (1.0f + expf(-z));
+    ref[i] = delta ? refine_box(delta[i], ref[i]) : 1.0f / (1.0f + expf(-ref[i]));
 }
 
 // target = om[idx]: ggml_get_rows of 256-wide token rows (src/ppdoclayout.cpp:805)

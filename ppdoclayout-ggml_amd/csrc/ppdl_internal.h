@@ -52,8 +52,12 @@ constexpr double kG[6][3] = {
 // row-major (A[m*lda + k], a_rowmajor = 1: token-major activations); B is a
 // dense k-major matrix or an implicit im2col view of a CHW image.
 // Epilogue: v = acc + bias[m or n]; v += add (add_mode 1); v = act(v);
-// v += add (add_mode 2); store at C[m*ldc + n], or C[n*ldc + m] when
-// c_trans (a CHW conv result written token-major).  `add` uses C's layout.
+// v += add (add_mode 2) or v = sigmoid(v + inv_sigmoid(add)) (add_mode 3, box
+// refinement; add may be C itself); store at C[m*ldc + n], or C[n*ldc + m]
+// when c_trans (a CHW conv result written token-major).  `add` uses C's
+// layout.  Prologue (row-major A, small-GEMM kernel only): for output columns
+// n < a_add_n the A operand is A + a_add (same lda), e.g. tokens + position
+// embedding in front of the q|k columns of a fused q|k|v projection.
 struct GemmArgs {
     const float *A;
     int64_t lda, sA;  // sA: batch stride (elements)
@@ -72,6 +76,8 @@ struct GemmArgs {
     // column (N itself, or N rounded up to 4 when ldb leaves room), 0 if not
     int n_vec;
     const float *add;
+    const float *a_add;  // nullptr: none; a_add_n is then ignored
+    int a_add_n;         // a multiple of 32
 };
 
 // act codes of the GEMM epilogue and the elementwise kernels
@@ -116,8 +122,8 @@ hipError_t im2col_ggml(const float *x, float *dst, int64_t IW, int64_t IH, int64
 
 // ---- decoder ops ----
 // val: 13125 token rows of 256 channels, row stride ldv (>= 256) floats
-hipError_t msdeform(const float *val, int ldv, const float *off, const float *awr, const float *ref,
-                    float *out, int nq, hipStream_t s);
+hipError_t msdeform(const float *val, int ldv, const float *off, int ldo, const float *awr, int ldw,
+                    const float *ref, float *out, int nq, hipStream_t s);
 hipError_t mask_box(const float *ml, float *out, int nq, hipStream_t s);
 // ws (optional, >= 8 * ntok bytes): per-token keys, computed grid-wide first
 hipError_t topk(const float *logits, int32_t *out, int ntok, int nc, int nq, void *ws, int64_t ws_bytes,

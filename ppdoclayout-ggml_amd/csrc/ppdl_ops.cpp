@@ -186,10 +186,11 @@ int check_op(const int32_t *p, const ppdl_tview *dst, const ppdl_tview *src, int
         }
         case PPDL_OP_MSDEF: {
             if (nsrc < 4 || !contig_f32(dst)) return PPDL_EINVAL;
-            // the value map may be a row-strided view (one slice of a wider projection)
-            if (!rows_f32(&src[0])) return PPDL_EINVAL;
-            for (int i = 1; i < 4; i++)
-                if (!contig_f32(&src[i])) return PPDL_EINVAL;
+            // value, offsets and weights may be row-strided views (slices of
+            // wider projections)
+            for (int i = 0; i < 3; i++)
+                if (!rows_f32(&src[i])) return PPDL_EINVAL;
+            if (!contig_f32(&src[3])) return PPDL_EINVAL;
             const int64_t NQ = dst->ne[1];
             if (!shape_is(dst, kDM, NQ, 1, 1) || !shape_is(&src[0], kDM, kNTOK, 1, 1) ||
                 !shape_is(&src[1], kNH * kNLVL * kNPTS * 2, NQ, 1, 1) ||
@@ -366,8 +367,8 @@ extern "C" PPDL_HIP_API int ppdl_hip_run(const int32_t op_params[16], const ppdl
         }
         case PPDL_OP_MSDEF:
             return status_of(msdeform((const float *)src[0].data, (int)(src[0].nb[1] / 4), (const float *)src[1].data,
-                                      (const float *)src[2].data, (const float *)src[3].data,
-                                      (float *)dst->data, (int)dst->ne[1], s));
+                                      (int)(src[1].nb[1] / 4), (const float *)src[2].data, (int)(src[2].nb[1] / 4),
+                                      (const float *)src[3].data, (float *)dst->data, (int)dst->ne[1], s));
         case PPDL_OP_MASKBOX:
             return status_of(mask_box((const float *)src[0].data, (float *)dst->data, (int)dst->ne[1], s));
         case PPDL_OP_TOPK: {

@@ -14,18 +14,12 @@
 // padding is never written by the input transform nor read by the output.  The
 // arithmetic is a fixed chain of fmaf over the nonzero matrix entries in
 // ascending index order, which the CPU oracle repeats exactly.
-#include "ppdl_internal.h"
+#include "device_math.h"
 
 namespace ppdl {
 namespace {
 
 constexpr int kThreads = 256;
-
-__device__ __forceinline__ float act_f(float v, int act) {
-    if (act == 1) return v > 0.0f ? v : 0.0f;
-    if (act == 2) return v / (1.0f + expf(-v));
-    return v;
-}
 
 // PAD = 0: x is the padded image (IWp x IHp), tile (ty,tx) reads rows 4ty..4ty+5.
 // PAD = 1: x is the unpadded image, the conv's pad of 1 is applied on the fly.

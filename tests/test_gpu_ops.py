@@ -455,22 +455,37 @@ def hip_msdeform(hip, val, off, awr, ref):
     return host(out)
 
 
+def col_slice_view(hip, wide, col, ncols):
+    """ne(ncols, rows) view of columns [col, col + ncols) of a 2-d tensor."""
+    rows, ld = wide.shape
+    v = hip.TView()
+    v.data = wide.data_ptr() + col * 4
+    for i, (n, b) in enumerate(zip((ncols, rows, 1, 1), (4, ld * 4, ld * 4 * rows, ld * 4 * rows))):
+        v.ne[i], v.nb[i] = n, b
+    v.type = hip.TYPE_F32
+    return v
+
+
 def test_msdeform_row_strided_value(hip, orc):
-    """The value map may be a row-strided slice of a wider projection (the
-    runtime's six decoder layers share one 13125 x 1536 projection): same
-    result, bit for bit, as the contiguous map."""
+    """Value map, offsets and attention logits may be row-strided slices of
+    wider projections (the runtime's six decoder layers share one 13125 x
+    1536 value projection; offsets | logits come from one 288-wide GEMM):
+    same result, bit for bit, as the contiguous inputs."""
     val, off, awr, ref = msdef_config4(np.random.default_rng(SEED + 44))
     wide = torch.full((val.shape[0], 1536), float("nan"), device="cuda")
     wide[:, 512:768] = dev(val)
-    v = hip.TView()
-    v.data = wide.data_ptr() + 512 * 4
-    for i, (n, b) in enumerate(zip((256, val.shape[0], 1, 1), (4, 1536 * 4, 1536 * 4 * val.shape[0],
-                                                                    1536 * 4 * val.shape[0]))):
-        v.ne[i], v.nb[i] = n, b
-    v.type = hip.TYPE_F32
+    v = col_slice_view(hip, wide, 512, 256)
     out = torch.empty((ref.shape[0], 256), device="cuda")
     hip.run_checked(hip.OP_MSDEF, out, [v, dev(off), dev(awr), dev(ref)])
-    assert np.array_equal(host(out), hip_msdeform(hip, val, off, awr, ref))
+    want = hip_msdeform(hip, val, off, awr, ref)
+    assert np.array_equal(host(out), want)
+    soaw = torch.full((ref.shape[0], 300), float("nan"), device="cuda")
+    soaw[:, :192] = dev(off)
+    soaw[:, 192:288] = dev(awr)
+    out2 = torch.empty((ref.shape[0], 256), device="cuda")
+    hip.run_checked(hip.OP_MSDEF, out2, [v, col_slice_view(hip, soaw, 0, 192), col_slice_view(hip, soaw, 192, 96),
+                                         dev(ref)])
+    assert np.array_equal(host(out2), want)
     bad = hip.TView()
     bad.data, bad.type = v.data, v.type
     for i, (n, b) in enumerate(zip((256, val.shape[0], 1, 1), (4, 255 * 4, 255 * 4 * val.shape[0],
