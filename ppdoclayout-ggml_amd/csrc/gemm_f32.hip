@@ -480,19 +480,47 @@ __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((((N >> 4) & 3) << 14) | (0xF << 8) | (0x7 << 4) | (N & 0xF));
 }
 
-// NS LDS stages: NS - 1 tiles in flight while one is computed (2 when many
-// blocks share a CU, deeper when few blocks must hide copy latency alone).
-template <int BM, int BN, int WGM, bool SPLIT, int NS>
-__global__ __launch_bounds__(kThreads) void k_gemm_dma(GemmArgs g, SplitArgs sp, int tiles_m, int tiles_mn) {
-    static_assert(NS >= 2 && NS <= 4, "stages");
+// global_load_lds_dwordx4 with a wave-uniform 64-bit base (SGPR pair) and a
+// 32-bit per-lane byte offset
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"  // m0 is reserved: nothing else in these kernels uses it
+__device__ __forceinline__ void dma16s(uint64_t base, uint32_t off, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base),
+                 "s"(__builtin_amdgcn_readfirstlane(lds))
+                 : "memory", "m0");
+}
+#pragma clang diagnostic pop
+// (readfirstlane returns int: each half goes through uint32_t, else the low
+// half would sign-extend into the high one)
+__device__ __forceinline__ uint64_t uniform_ptr(const float *p) {
+    const uint64_t v = (uint64_t)(uintptr_t)p;
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)v);
+    return ((uint64_t)hi << 32) | lo;
+}
+
+// NS LDS stages: NS - 1 tiles in flight while one is computed.  KG wave
+// groups: KG = 2 runs 8 waves per block, group g contracting the k rows
+// [16g, 16g + 16) of every tile, and sums the two partial tiles through LDS
+// before the epilogue (twice the waves per SIMD for the same tile count).
+// One loop body per k tile (the stage is a runtime index): a body duplicated
+// per stage let the compiler move the accumulators between register files at
+// every tile.  A wave reads all of its fragments of a tile before the tile's
+// MFMAs, so the chain waits for LDS once per tile.
+template <int BM, int BN, int WGM, bool SPLIT, int NS, int KG>
+__global__ __launch_bounds__(kThreads * KG) void k_gemm_dma(GemmArgs g, SplitArgs sp, int tiles_m, int tiles_mn) {
+    static_assert(NS >= 2 && NS <= 4 && (KG == 1 || KG == 2), "stages / groups");
+    constexpr int NT = kThreads * KG;
     constexpr int WGN = 4 / WGM, WM = BM / WGM, WN = BN / WGN, TM = WM / 32, TN = WN / 32;
-    constexpr int IA = kBK * BM / 4 / kThreads, IB = kBK * BN / 4 / kThreads;  // copies per wave per tile
-    constexpr int KH = kBK / 2, NP = KH / 2;
+    constexpr int IA = kBK * BM / 4 / NT, IB = kBK * BN / 4 / NT;  // copies per wave per tile
+    constexpr int KH = kBK / 2, KQ = KH / KG;                       // k rows per half-wave and group
     static_assert(IA >= 1 && IB >= 1 && TM >= 1 && TN >= 1, "bad tile");
-    __shared__ __attribute__((aligned(1024))) float As[NS][kBK * BM];
-    __shared__ __attribute__((aligned(1024))) float Bs[NS][kBK * BN];
+    constexpr int SA = kBK * BM, SB = kBK * BN;  // stage sizes (floats)
+    __shared__ __attribute__((aligned(1024))) float smem[NS * (SA + SB)];
+    float *const As = smem, *const Bs = smem + NS * SA;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int grp = wave >> 2, wq = wave & 3;  // k group, position in the 2-d wave grid
     const int logical = xcd_remap(blockIdx.x, gridDim.x);
     const int S = SPLIT ? sp.splits : 1;
     const int split = SPLIT ? logical % S : 0;
@@ -505,8 +533,7 @@ __global__ __launch_bounds__(kThreads) void k_gemm_dma(GemmArgs g, SplitArgs sp,
     const int kt0 = SPLIT ? split * sp.ktiles_per_split : 0;
     const int kt1 = SPLIT ? min(nk_total, kt0 + sp.ktiles_per_split) : nk_total;
     const int nk = kt1 - kt0;
-    const float *__restrict__ A = g.A + (int64_t)bz * g.sA;
-    const float *__restrict__ B = g.B + (int64_t)bz * g.sB;
+    const uint64_t Ab = uniform_ptr(g.A + (int64_t)bz * g.sA), Bb = uniform_ptr(g.B + (int64_t)bz * g.sB);
     const int lda = (int)g.lda, ldb = (int)g.ldb;
 
     // this lane's chunk of each copy: tile row and clamped column
@@ -523,14 +550,21 @@ __global__ __launch_bounds__(kThreads) void k_gemm_dma(GemmArgs g, SplitArgs sp,
         br[e] = c / (BN / 4);
         bc[e] = min(n0 + (c % (BN / 4)) * 4, g.n_vec - 4);
     }
+    // byte offsets (dispatch keeps them below 2^32); rows past K are clamped
+    // to K - 1 on the tile that reaches the end of K
     auto issue = [&](int s, int kt) {
         const int k0 = kt * kBK;
+        const bool full = k0 + kBK <= K;
 #pragma unroll
-        for (int e = 0; e < IA; e++)
-            dma16(A + (uint32_t)(min(k0 + ar[e], K - 1) * lda + ac[e]), lds_off(&As[s][(wave * IA + e) * 256]));
+        for (int e = 0; e < IA; e++) {
+            const int row = full ? k0 + ar[e] : min(k0 + ar[e], K - 1);
+            dma16s(Ab, (uint32_t)(row * lda + ac[e]) * 4u, lds_off(As + s * SA + (wave * IA + e) * 256));
+        }
 #pragma unroll
-        for (int e = 0; e < IB; e++)
-            dma16(B + (uint32_t)(min(k0 + br[e], K - 1) * ldb + bc[e]), lds_off(&Bs[s][(wave * IB + e) * 256]));
+        for (int e = 0; e < IB; e++) {
+            const int row = full ? k0 + br[e] : min(k0 + br[e], K - 1);
+            dma16s(Bb, (uint32_t)(row * ldb + bc[e]) * 4u, lds_off(Bs + s * SB + (wave * IB + e) * 256));
+        }
     };
 
     f32x16 acc[TM][TN];
@@ -540,44 +574,31 @@ __global__ __launch_bounds__(kThreads) void k_gemm_dma(GemmArgs g, SplitArgs sp,
         for (int j = 0; j < TN; j++)
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
-    const int wm0 = (wave % WGM) * WM, wn0 = (wave / WGM) * WN;
-    const int l32 = lane & 31, lk = (lane >> 5) * KH;
+    const int wm0 = (wq % WGM) * WM, wn0 = (wq / WGM) * WN;
+    const int l32 = lane & 31;
+    // this half-wave's k rows of a tile: kr .. kr + 2*KQ... (lanes 32-63 from row 16)
+    const int kr = (lane >> 5) * KH + KQ * grp;
 
+    // one tile: rows kr + q, q < KQ, as MFMA k-slot (lane >> 5) of step q
     auto compute = [&](int s) {
-        float2 fa[NP][TM], fb[NP][TN];
-        auto rd = [&](int p) {
+        const float *as = As + s * SA + kr * BM + wm0 + l32;
+        const float *bs = Bs + s * SB + kr * BN + wn0 + l32;
+        float fa[KQ][TM], fb[KQ][TN];
 #pragma unroll
-            for (int i = 0; i < TM; i++) {
-                fa[p][i].x = As[s][(lk + 2 * p) * BM + wm0 + i * 32 + l32];
-                fa[p][i].y = As[s][(lk + 2 * p + 1) * BM + wm0 + i * 32 + l32];
-            }
+        for (int q = 0; q < KQ; q++) {
 #pragma unroll
-            for (int j = 0; j < TN; j++) {
-                fb[p][j].x = Bs[s][(lk + 2 * p) * BN + wn0 + j * 32 + l32];
-                fb[p][j].y = Bs[s][(lk + 2 * p + 1) * BN + wn0 + j * 32 + l32];
-            }
-        };
-        rd(0);
-        rd(1);
-        __builtin_amdgcn_sched_group_barrier(0x100, 2 * (TM + TN), 0);
+            for (int i = 0; i < TM; i++) fa[q][i] = as[q * BM + i * 32];
 #pragma unroll
-        for (int p = 0; p < NP; p++) {
-#pragma unroll
-            for (int i = 0; i < TM; i++)
-#pragma unroll
-                for (int j = 0; j < TN; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[p][i].x, fb[p][j].x, acc[i][j], 0, 0, 0);
-#pragma unroll
-            for (int i = 0; i < TM; i++)
-#pragma unroll
-                for (int j = 0; j < TN; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[p][i].y, fb[p][j].y, acc[i][j], 0, 0, 0);
-            __builtin_amdgcn_sched_group_barrier(0x008, 2 * TM * TN, 0);
-            if (p + 2 < NP) {
-                rd(p + 2);
-                __builtin_amdgcn_sched_group_barrier(0x100, TM + TN, 0);
-            }
+            for (int j = 0; j < TN; j++) fb[q][j] = bs[q * BN + j * 32];
         }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int q = 0; q < KQ; q++)
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int j = 0; j < TN; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[q][i], fb[q][j], acc[i][j], 0, 0, 0);
     };
 
     if (nk > 0) {
@@ -585,25 +606,42 @@ __global__ __launch_bounds__(kThreads) void k_gemm_dma(GemmArgs g, SplitArgs sp,
         const int ktail = K - (nk_total - 1) * kBK;  // valid rows of the global last tile
 #pragma unroll
         for (int u = 0; u < NS - 1; u++) issue(u, min(kt0 + u, klast));
-        for (int it = 0; it < nk; it += NS) {
-#pragma unroll
-            for (int u = 0; u < NS; u++) {
-                if (it + u < nk) {
-                    const int kt = kt0 + it + u;
-                    // this wave's copies of tile kt have landed (NS - 2 younger
-                    // tiles may stay in flight) ...
-                    wait_vmcnt<(NS - 2) * (IA + IB)>();
-                    __syncthreads();  // ... and everyone's; tile kt-1 is consumed
-                    if (kt == nk_total - 1 && ktail < kBK) {
-                        for (int i = tid; i < (kBK - ktail) * BM; i += kThreads) As[u][ktail * BM + i] = 0.0f;
-                        __syncthreads();
-                    }
-                    issue((u + NS - 1) % NS, min(kt + NS - 1, klast));  // into tile kt-1's stage
-                    compute(u);
-                }
+        for (int i = 0; i < nk; i++) {
+            const int kt = kt0 + i, u = i % NS;
+            // this wave's copies of tile kt have landed (NS - 2 younger tiles
+            // may stay in flight) ...
+            wait_vmcnt<(NS - 2) * (IA + IB)>();
+            __syncthreads();  // ... and everyone's; tile kt-1 is consumed
+            if (kt == nk_total - 1 && ktail < kBK) {
+                for (int x = tid; x < (kBK - ktail) * BM; x += NT) As[u * SA + ktail * BM + x] = 0.0f;
+                __syncthreads();
             }
+            issue((i + NS - 1) % NS, min(kt + NS - 1, klast));  // into tile kt-1's stage
+            compute(u);
         }
         wait_vmcnt<0>();  // no copy may still target this block's LDS when it exits
+    }
+    if constexpr (KG == 2) {
+        // group 1's partial tile joins group 0's through the (now idle) stages
+        static_assert(4 * TM * TN * 16 * 64 <= NS * (SA + SB), "reduction space");
+        __syncthreads();  // every wave's last compute() has read its operands
+        float *red = smem + wq * (TM * TN * 16 * 64) + lane;
+        if (grp == 1) {
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int j = 0; j < TN; j++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++) red[((i * TN + j) * 16 + r) * 64] = acc[i][j][r];
+        }
+        __syncthreads();
+        if (grp == 1) return;
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < TN; j++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) acc[i][j][r] += red[((i * TN + j) * 16 + r) * 64];
     }
     gemm_epilogue<TM, TN, SPLIT>(acc, g, sp, split, bz, m0 + wm0, n0 + wn0, lane);
 }
@@ -913,7 +951,7 @@ int small_waves(int K, int64_t tiles) {
     const char *e = getenv("PPDL_SMALL_WV");
     if (e && *e) {
         const int w = atoi(e);
-        if (w == 4 || w == 8 || w == 16) return w;
+        if (w == 1 || w == 2 || w == 4 || w == 8 || w == 16) return w;
     }
     const int nchunk = (K + kSmallKC - 1) / kSmallKC;
     if (tiles >= 256 || nchunk <= 4) return 4;
@@ -1004,33 +1042,33 @@ bool dma_ok(const GemmArgs &g) {
         return e && e[0] == '0';
     }();
     const auto a16 = [](const void *p) { return (((uintptr_t)p) & 15) == 0; };
+    // copies address one batch plane with 32-bit byte offsets
+    const bool fits = ((int64_t)g.K * g.lda + g.M) * 4 < (1LL << 32) && ((int64_t)g.K * g.ldb + g.N + 4) * 4 < (1LL << 32);
     return !off && !g.a_rowmajor && g.M >= 4 && g.M % 4 == 0 && n_vec_of(g) >= 4 && g.lda % 4 == 0 &&
-           g.ldb % 4 == 0 && g.sA % 4 == 0 && g.sB % 4 == 0 && a16(g.A) && a16(g.B);
+           g.ldb % 4 == 0 && g.sA % 4 == 0 && g.sB % 4 == 0 && a16(g.A) && a16(g.B) && fits;
 }
 
-// LDS stages of the direct-to-LDS kernel: deeper when the launch leaves
-// fewer than ~2 blocks per CU (each block must hide its own copy latency)
-int dma_stages(int64_t blocks) {
-    static const int64_t low = env_int("PPDL_DMA_LOW_BLOCKS", 512);
-    static const int deep = (int)env_int("PPDL_DMA_NS", 2);
-    return blocks < low ? deep : 2;
+// Wave groups of the direct-to-LDS kernel: 2 (8 waves per block) where each
+// wave still gets a 16-byte copy per operand; PPDL_DMA_KG=1 keeps 4 waves.
+// Measured on the network: 3.864 -> 3.859 ms; single 1x1 convs up to 14%
+// (K=512 N=10000 M=512: 83 -> 95 TF/s), none slower by more than noise.
+int dma_groups() {
+    static const int kg = (int)env_int("PPDL_DMA_KG", 2);
+    return kg == 1 ? 1 : 2;
 }
 
 template <int BM, int BN, int WGM, bool SPLIT>
 void launch_dma(const GemmArgs &g, const SplitArgs &sp, int64_t total, int tiles_m, int tiles_n, hipStream_t s) {
-    switch (dma_stages(total)) {
-        case 3:
-            hipLaunchKernelGGL((k_gemm_dma<BM, BN, WGM, SPLIT, 3>), dim3((unsigned)total), dim3(kThreads), 0, s, g,
-                               sp, tiles_m, tiles_m * tiles_n);
-            break;
-        case 4:
-            hipLaunchKernelGGL((k_gemm_dma<BM, BN, WGM, SPLIT, 4>), dim3((unsigned)total), dim3(kThreads), 0, s, g,
-                               sp, tiles_m, tiles_m * tiles_n);
-            break;
-        default:
-            hipLaunchKernelGGL((k_gemm_dma<BM, BN, WGM, SPLIT, 2>), dim3((unsigned)total), dim3(kThreads), 0, s, g,
-                               sp, tiles_m, tiles_m * tiles_n);
+    // 8 waves need at least one 16-byte copy per operand and wave
+    if constexpr (kBK * BM / 4 >= 2 * kThreads && kBK * BN / 4 >= 2 * kThreads) {
+        if (dma_groups() == 2) {
+            hipLaunchKernelGGL((k_gemm_dma<BM, BN, WGM, SPLIT, 2, 2>), dim3((unsigned)total), dim3(2 * kThreads), 0,
+                               s, g, sp, tiles_m, tiles_m * tiles_n);
+            return;
+        }
     }
+    hipLaunchKernelGGL((k_gemm_dma<BM, BN, WGM, SPLIT, 2, 1>), dim3((unsigned)total), dim3(kThreads), 0, s, g, sp,
+                       tiles_m, tiles_m * tiles_n);
 }
 
 template <int BM, int BN, int WGM, int AMODE, int BMODE>
@@ -1075,7 +1113,9 @@ hipError_t launch(const GemmArgs &g, int S, const GemmWorkspace &ws, hipStream_t
 
 template <int AMODE, bool PRE>
 hipError_t launch_small_wv(const GemmArgs &g, int wv, dim3 grid, int tiles_m, int tmn, hipStream_t s) {
-    if (wv == 4) hipLaunchKernelGGL((k_gemm_small<AMODE, 4, PRE>), grid, dim3(256), 0, s, g, tiles_m, tmn);
+    if (wv == 1) hipLaunchKernelGGL((k_gemm_small<AMODE, 1, PRE>), grid, dim3(64), 0, s, g, tiles_m, tmn);
+    else if (wv == 2) hipLaunchKernelGGL((k_gemm_small<AMODE, 2, PRE>), grid, dim3(128), 0, s, g, tiles_m, tmn);
+    else if (wv == 4) hipLaunchKernelGGL((k_gemm_small<AMODE, 4, PRE>), grid, dim3(256), 0, s, g, tiles_m, tmn);
     else if (wv == 8) hipLaunchKernelGGL((k_gemm_small<AMODE, 8, PRE>), grid, dim3(512), 0, s, g, tiles_m, tmn);
     else hipLaunchKernelGGL((k_gemm_small<AMODE, 16, PRE>), grid, dim3(1024), 0, s, g, tiles_m, tmn);
     return hipGetLastError();

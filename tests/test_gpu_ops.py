@@ -175,13 +175,13 @@ def test_conv1x1_shapes(hip, orc, IC, H, W, OC, act):
     assert normwise(y, orc.conv2d_f64(x, w, b, 1, 0, act)) < TOL
 
 
-@pytest.mark.parametrize("wv", ["", "4", "8", "16"])
+@pytest.mark.parametrize("wv", ["", "1", "2", "4", "8", "16"])
 @pytest.mark.parametrize("IC,H,W,OC", [
     (1, 1, 1, 1), (3, 7, 5, 2), (17, 13, 11, 33), (256, 15, 20, 256), (1024, 17, 19, 96), (70, 9, 9, 300),
 ])
 def test_small_gemm_kernel(hip, orc, IC, H, W, OC, wv, monkeypatch):
-    """The small-GEMM kernel (32x32 tiles, K split over the block's 4, 8 or
-    16 waves; "" = the planner's choice from K) forced for every GEMM, on edge
+    """The small-GEMM kernel (32x32 tiles, K split over the block's 1 to 16
+    waves; "" = the planner's choice from K) forced for every GEMM, on edge
     shapes: K not a multiple of the 32-wide chunk, fewer chunks than waves, M
     and N not multiples of 32."""
     monkeypatch.setenv("PPDL_GEMM_TILE", "6,1")
