@@ -1209,12 +1209,14 @@ std::string gemm_kernel_name(const GemmArgs &g, int64_t ws_bytes, bool im2col) {
     int bm = kCfgs[p.cfg].bm, bn = kCfgs[p.cfg].bn, wgm = kCfgs[p.cfg].wgm;
     if (g.a_rowmajor && p.cfg != 5) bm = 64, bn = 64, wgm = 2;  // the two row-major-A shapes
     char buf[96];
-    if (!im2col && dma_ok(g))
-        snprintf(buf, sizeof(buf), "k_gemm_dma<%d, %d, %d, %s>%s", bm, bn, wgm, p.splits > 1 ? "true" : "false",
-                 p.splits > 1 ? "+k_splitk_reduce" : "");
-    else
+    if (!im2col && dma_ok(g)) {
+        const int kg = (kBK * bm / 4 >= 2 * kThreads && kBK * bn / 4 >= 2 * kThreads) ? dma_groups() : 1;
+        snprintf(buf, sizeof(buf), "k_gemm_dma<%d, %d, %d, %s, 2, %d>%s", bm, bn, wgm, p.splits > 1 ? "true" : "false",
+                 kg, p.splits > 1 ? "+k_splitk_reduce" : "");
+    } else {
         snprintf(buf, sizeof(buf), "k_gemm<%d, %d, %d, %d, %d, %s>%s", bm, bn, wgm, g.a_rowmajor ? 1 : 0,
                  im2col ? 1 : 0, p.splits > 1 ? "true" : "false", p.splits > 1 ? "+k_splitk_reduce" : "");
+    }
     return buf;
 }
 hipError_t gemm_im2col(const GemmArgs &g, const GemmWorkspace &ws, hipStream_t s) { return dispatch<1>(g, ws, s); }
