@@ -293,8 +293,9 @@ __global__ __launch_bounds__(kThreads) void k_gemm(GemmArgs g, SplitArgs sp, int
     // it, and one past it is clamped to the last valid float4 (finite values
     // in rows / columns the epilogue never stores).  Other edge tiles load
     // clamped scalars.
-    auto body = [&](auto edge_tag) {
+    auto body = [&](auto edge_tag, auto tap_tag) {
         constexpr bool EDGE = decltype(edge_tag)::value;
+        constexpr bool ONE_TAP = decltype(tap_tag)::value;  // im2col with IC % kBK == 0
         auto load = [&](St &r, int kt) {
             const int k0 = kt * kBK;
             if (AMODE == 0) {
@@ -335,6 +336,20 @@ __global__ __launch_bounds__(kThreads) void k_gemm(GemmArgs g, SplitArgs sp, int
                         r.b4[e].w = row[min(gn4 + 3, N - 1)];
                     }
                 }
+            } else if (ONE_TAP) {
+                // the whole k tile is one tap (IC % kBK == 0, K % kBK == 0): one
+                // bounds test per tile, rows RB1 channels apart.  A lane outside
+                // the image reads a clamped in-image address (its value is
+                // masked at the store), not one shared address.
+                const int tap = k0 / g.IC;
+                const int kh = tap / g.KW, kw = tap - kh * g.KW;
+                const int iy = iy0 + kh, ix = ix0 + kw;
+                const bool ok = bn_ok && iy >= 0 && iy < g.IH && ix >= 0 && ix < g.IW;
+                const uint32_t base = (uint32_t)((k0 - tap * g.IC + bk1) * plane +
+                                                 min(max(iy, 0), g.IH - 1) * g.IW + min(max(ix, 0), g.IW - 1));
+#pragma unroll
+                for (int e = 0; e < EB1; e++) r.b1[e] = B[base + (uint32_t)(e * RB1 * plane)];
+                r.ok1 = ok ? 0xFFFFFFFFu : 0u;
             } else {
                 // k = (kh*KW + kw)*IC + ic: decompose the first row once, then
                 // step ic by RB1 with carries into kw and kh
@@ -440,10 +455,19 @@ __global__ __launch_bounds__(kThreads) void k_gemm(GemmArgs g, SplitArgs sp, int
     };
     const bool edge_m = AMODE == 0 && m0 + BM > M && (M & 3) != 0;  // row-major A clamps rows itself
     const bool edge_n = BMODE == 0 && n0 + BN > N && g.n_vec == 0;  // im2col B masks per element
-    if (edge_m || edge_n)
-        body(std::true_type{});
-    else
-        body(std::false_type{});
+    if constexpr (BMODE == 1) {
+        const bool one_tap = g.IC % kBK == 0 && K % kBK == 0;
+        if (edge_m || edge_n) {
+            if (one_tap) body(std::true_type{}, std::true_type{});
+            else body(std::true_type{}, std::false_type{});
+        } else {
+            if (one_tap) body(std::false_type{}, std::true_type{});
+            else body(std::false_type{}, std::false_type{});
+        }
+    } else {
+        if (edge_m || edge_n) body(std::true_type{}, std::false_type{});
+        else body(std::false_type{}, std::false_type{});
+    }
 
     gemm_epilogue<TM, TN, SPLIT>(acc, g, sp, split, bz, m0 + wm0, n0 + wn0, lane);
 }

@@ -270,6 +270,8 @@ IM2COL_CONFIGS = [  # IC, IH, IW, OC, K, S, P
     (256, 100, 100, 256, 3, 2, 1),
     (256, 50, 50, 256, 3, 2, 1),
     (3, 800, 800, 32, 3, 2, 1),
+    (32, 401, 401, 16, 2, 1, 0),    # stem2a: one tap per k tile (IC % 32 == 0)
+    (64, 400, 400, 32, 3, 2, 1),    # stem3: one tap per k tile
 ]
 
 
@@ -286,7 +288,10 @@ def test_conv_im2col_config3(hip, orc, IC, IH, IW, OC, K, S, P, act):
 
 
 @pytest.mark.parametrize("IC,IH,IW,OC,K,S,P", [(1, 1, 1, 1, 1, 1, 0), (2, 5, 3, 3, 2, 1, 0), (7, 9, 8, 5, 3, 2, 1),
-                                               (16, 33, 31, 70, 3, 2, 1), (4, 6, 6, 9, 5, 1, 2), (3, 2, 2, 4, 3, 1, 1)])
+                                               (16, 33, 31, 70, 3, 2, 1), (4, 6, 6, 9, 5, 1, 2), (3, 2, 2, 4, 3, 1, 1),
+                                               # one tap per k tile (IC % 32 == 0), ragged M / N and borders
+                                               (32, 33, 31, 40, 3, 2, 1), (64, 17, 19, 20, 2, 1, 0),
+                                               (32, 9, 9, 7, 3, 1, 1), (96, 5, 4, 33, 3, 1, 1)])
 def test_conv_im2col_shapes(hip, orc, IC, IH, IW, OC, K, S, P):
     say(f"im2col conv edge k{K}s{S}p{P} {IC}->{OC} @{IH}x{IW}")
     rng = np.random.default_rng(IC + IH + IW + OC + K)
