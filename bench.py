@@ -8,9 +8,11 @@ synthetic document page.  One step is one hipGraph replay of the whole graph
 device time per image from HIP events on the replay stream.
 
 The metric's second half, conv GEMM TFLOPS as a fraction of the FP32 matrix
-peak, comes from the per-node profile (ppdl_profile_nodes: every node run
-eagerly between HIP events on the graph's stream): algorithmic conv GEMM FLOP
-(Winograd counted at its 36-plane GEMM) over the conv GEMM nodes' time.
+peak, comes from the per-node profile (ppdl_profile_nodes: every node
+captured `kernel_reps` times into a graph of its own and replayed between HIP
+events on the graph's stream, so no host launch cost is counted): algorithmic
+conv GEMM FLOP (Winograd counted at its 36-plane GEMM) over the conv GEMM
+nodes' time.
 
 roofline: the GEMM kernel with the largest total time in one image, its
 algorithmic FLOP per launch over its mean launch time; traffic is its HBM

@@ -82,8 +82,9 @@ PPDL_API double ppdl_time_graph(ppdl_ctx * ctx, int iters);
 /* Number of kernel nodes one graph replay executes (0 if not built). */
 PPDL_API int ppdl_graph_nodes(ppdl_ctx * ctx);
 
-/* Per-node device time of the graph: each node (one layer's kernels) is run
- * eagerly `iters` times between two HIP events on the graph's stream. */
+/* Per-node device time of the graph: each node (one layer's kernels) is
+ * captured `iters` times into a graph of its own, replayed between two HIP
+ * events on the graph's stream (in-graph launch cost, no host launch cost). */
 typedef struct {
     char    name[64];    /* layer / node name                                   */
     char    kernel[64];  /* GEMM nodes: the device kernel(s) the plan launches   */

@@ -927,10 +927,12 @@ double Net::time_graph(int iters) {
     return good ? (double)ms / iters : -1.0;
 }
 
-// Each node run eagerly `iters` times between two HIP events on the graph's
-// stream (after two untimed runs): the per-node device time the graph is made
-// of.  Nodes that update a buffer in place drift its contents meanwhile; the
-// next ppdl_infer / ppdl_compute recomputes everything from the image.
+// Per-node device time as the graph sees it: each node is captured `iters`
+// times into a graph of its own, which is replayed once untimed and once
+// between two HIP events on the graph's stream.  (Eager launches would add
+// the host's per-launch cost, several µs, to every short kernel.)  Nodes that
+// update a buffer in place drift its contents meanwhile; the next ppdl_infer /
+// ppdl_compute recomputes everything from the image.
 int Net::profile_nodes(int iters, ppdl_node_stat *out, int cap) {
     hipEvent_t e0, e1;
     if (iters < 1 || hipEventCreate(&e0) != hipSuccess) return -1;
@@ -943,12 +945,20 @@ int Net::profile_nodes(int iters, ppdl_node_stat *out, int cap) {
     for (size_t i = 0; good && i < nodes_.size() && n < cap; i++) {
         Node &nd = nodes_[i];
         if (nd.kind != 0) continue;
-        for (int r = 0; good && r < 2; r++) good = nd.run(stream_) == 0;
-        good = good && hipEventRecord(e0, stream_) == hipSuccess;
-        for (int r = 0; good && r < iters; r++) good = nd.run(stream_) == 0;
+        hipGraph_t g = nullptr;
+        hipGraphExec_t ge = nullptr;
+        good = hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal) == hipSuccess;
+        bool ran = good;
+        for (int r = 0; ran && r < iters; r++) ran = nd.run(stream_) == 0;
+        good = good && hipStreamEndCapture(stream_, &g) == hipSuccess && ran;  // capture always ended
+        good = good && hipGraphInstantiate(&ge, g, nullptr, nullptr, 0) == hipSuccess;
+        good = good && hipGraphLaunch(ge, stream_) == hipSuccess;
+        good = good && hipEventRecord(e0, stream_) == hipSuccess && hipGraphLaunch(ge, stream_) == hipSuccess;
         good = good && hipEventRecord(e1, stream_) == hipSuccess && hipEventSynchronize(e1) == hipSuccess;
         float ms = 0.0f;
         good = good && hipEventElapsedTime(&ms, e0, e1) == hipSuccess;
+        if (ge) (void)hipGraphExecDestroy(ge);
+        if (g) (void)hipGraphDestroy(g);
         ppdl_node_stat &o = out[n++];
         memset(&o, 0, sizeof(o));
         snprintf(o.name, sizeof(o.name), "%s", nd.name.c_str());
