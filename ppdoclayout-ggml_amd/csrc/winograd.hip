@@ -26,7 +26,7 @@ constexpr int kThreads = 256;
 template <int PAD>
 __global__ __launch_bounds__(kThreads) void k_wg4_input(const float *__restrict__ x,
                                                         float *__restrict__ dt, int IW, int IH,
-                                                        int IC, int TW, int TH, int ldt) {
+                                                        int IC, int TW, int TH, int ldt, int vec) {
     const int T = TW * TH;
     const int64_t idx = (int64_t)blockIdx.x * kThreads + threadIdx.x;
     if (idx >= (int64_t)T * IC) return;
@@ -36,16 +36,39 @@ __global__ __launch_bounds__(kThreads) void k_wg4_input(const float *__restrict_
     const float *__restrict__ xc = x + (int64_t)ic * IH * IW;
 
     float d[6][6];
+    if (PAD && vec) {
+        // rows as one aligned float4 (columns 4tx .. 4tx+3, inside the row:
+        // the host sets vec only for IW % 4 == 0 and a 16-byte aligned x)
+        // plus the two halo columns: 18 loads, not 36.
+        // Out-of-image rows / columns read a clamped in-image address and are
+        // zeroed by select.
+        const bool left = tx > 0, right = 4 * tx + 4 < IW;
 #pragma unroll
-    for (int a = 0; a < 6; a++) {
-        const int iy = 4 * ty - PAD + a;
+        for (int a = 0; a < 6; a++) {
+            const int iy = 4 * ty - 1 + a;
+            const bool rin = iy >= 0 && iy < IH;
+            const float *row = xc + (int64_t)min(max(iy, 0), IH - 1) * IW + 4 * tx;
+            const float4 v = *reinterpret_cast<const float4 *>(row);
+            const float l = row[left ? -1 : 0], r = row[right ? 4 : 3];
+            d[a][0] = rin && left ? l : 0.0f;
+            d[a][1] = rin ? v.x : 0.0f;
+            d[a][2] = rin ? v.y : 0.0f;
+            d[a][3] = rin ? v.z : 0.0f;
+            d[a][4] = rin ? v.w : 0.0f;
+            d[a][5] = rin && right ? r : 0.0f;
+        }
+    } else {
 #pragma unroll
-        for (int b = 0; b < 6; b++) {
-            const int ix = 4 * tx - PAD + b;
-            if (PAD) {
-                d[a][b] = (iy >= 0 && iy < IH && ix >= 0 && ix < IW) ? xc[(int64_t)iy * IW + ix] : 0.0f;
-            } else {
-                d[a][b] = xc[(int64_t)iy * IW + ix];
+        for (int a = 0; a < 6; a++) {
+            const int iy = 4 * ty - PAD + a;
+#pragma unroll
+            for (int b = 0; b < 6; b++) {
+                const int ix = 4 * tx - PAD + b;
+                if (PAD) {
+                    d[a][b] = (iy >= 0 && iy < IH && ix >= 0 && ix < IW) ? xc[(int64_t)iy * IW + ix] : 0.0f;
+                } else {
+                    d[a][b] = xc[(int64_t)iy * IW + ix];
+                }
             }
         }
     }
@@ -140,10 +163,11 @@ hipError_t wg4_input(const float *x, float *dt, int IW, int IH, int IC, int TW, 
                      hipStream_t s) {
     const int64_t n = (int64_t)TW * TH * IC;
     const unsigned blocks = (unsigned)((n + kThreads - 1) / kThreads);
+    const int vec = (IW % 4 == 0 && (((uintptr_t)x) & 15) == 0) ? 1 : 0;
     if (pad)
-        hipLaunchKernelGGL(k_wg4_input<1>, dim3(blocks), dim3(kThreads), 0, s, x, dt, IW, IH, IC, TW, TH, ldt);
+        hipLaunchKernelGGL(k_wg4_input<1>, dim3(blocks), dim3(kThreads), 0, s, x, dt, IW, IH, IC, TW, TH, ldt, vec);
     else
-        hipLaunchKernelGGL(k_wg4_input<0>, dim3(blocks), dim3(kThreads), 0, s, x, dt, IW, IH, IC, TW, TH, ldt);
+        hipLaunchKernelGGL(k_wg4_input<0>, dim3(blocks), dim3(kThreads), 0, s, x, dt, IW, IH, IC, TW, TH, ldt, 0);
     return hipGetLastError();
 }
 

@@ -199,6 +199,28 @@ def test_small_gemm_kernel(hip, orc, IC, H, W, OC, wv, monkeypatch):
         assert normwise(host(wo), orc.conv2d_ref(x3, w3, b3, 1, 1, 1)) < TOL
 
 
+@pytest.mark.parametrize("IC,H,W", [(48, 200, 200), (5, 9, 12), (3, 4, 4), (7, 13, 8)])
+def test_wg4_input_vector_loads(hip, orc, IC, H, W):
+    """Op 15 on a 16-byte aligned image with W % 4 == 0 loads rows as float4 +
+    halo scalars; a 4-byte offset copy of the same image takes the scalar
+    path.  The transforms must agree bit for bit."""
+    say(f"wg4 input vector vs scalar {IC} @{H}x{W}")
+    x = np.random.default_rng(IC + H + W).standard_normal((IC, H, W)).astype(np.float32)
+    TW, TH = (W + 3) // 4, (H + 3) // 4
+    T = TW * TH
+    buf = torch.zeros(IC * H * W + 4, device="cuda")
+    outs = []
+    for off in (0, 1):  # 0: aligned (vector path), 1: 4-byte offset (scalar path)
+        xv = buf[off:off + IC * H * W].view(IC, H, W)
+        xv.copy_(dev(x))
+        assert (xv.data_ptr() % 16 == 0) == (off == 0)
+        dt = torch.full((36, IC, T), float("nan"), device="cuda")
+        hip.run_checked(hip.OP_WG4_INPUT_PAD, dt, [xv], T, TH)
+        outs.append(host(dt))
+    assert np.array_equal(outs[0], outs[1])
+    assert np.array_equal(outs[0], orc.wg4_input(x, TW, TH, 1))
+
+
 # ---------------------------------------------------------------- Winograd F(4,3)
 @pytest.mark.parametrize("IC,H,W,OC", [(64, 100, 100, 48), (96, 50, 50, 96), (256, 25, 25, 256), (7, 9, 11, 5)])
 def test_winograd_padded_planes(hip, orc, IC, H, W, OC):
