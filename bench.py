@@ -248,19 +248,22 @@ def run_network(args):
 
 # ---------------------------------------------------------------- op suite
 def time_nodes(suite, stream, reps):
-    """Average device time (us) of each suite node: `reps` back-to-back
-    launches between two HIP events recorded on the launch stream."""
+    """Average device time (us) of each suite node: the node captured `reps`
+    times into a graph of its own, one replay between two HIP events on the
+    launch stream (no host launch cost per kernel)."""
     import torch
 
     out = {}
     for n in suite.nodes:
-        for _ in range(3):
-            n.launch(stream.cuda_stream)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            for _ in range(reps):
+                n.launch(stream.cuda_stream)
+        g.replay()
         e0 = torch.cuda.Event(enable_timing=True)
         e1 = torch.cuda.Event(enable_timing=True)
         e0.record(stream)
-        for _ in range(reps):
-            n.launch(stream.cuda_stream)
+        g.replay()
         e1.record(stream)
         e1.synchronize()
         out[n.name] = e0.elapsed_time(e1) * 1000.0 / reps
@@ -412,7 +415,7 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", choices=["network", "conv_suite"], default="network")
-    ap.add_argument("--kernel-reps", type=int, default=10, help="eager runs per node in the per-node profile")
+    ap.add_argument("--kernel-reps", type=int, default=10, help="runs per node in the per-node profile (captured into one graph)")
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU baseline work")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--calib-copy-mib", type=int, default=0,

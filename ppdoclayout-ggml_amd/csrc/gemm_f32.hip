@@ -165,7 +165,10 @@ __device__ __forceinline__ void gemm_epilogue(const f32x16 (&acc)[TM][TN], const
 }
 
 // AMODE 0: A k-major; AMODE 1: A row-major (K % 4 == 0, lda % 4 == 0).
-// BMODE 0: dense B; BMODE 1: implicit im2col B.
+// BMODE 0: dense B; BMODE 1: implicit im2col B (generic, or one kernel tap
+// per k tile when IC % kBK == 0); BMODE 2: implicit im2col B with IC >= kBK,
+// at most two taps per k tile (its own instantiation: its loader needs more
+// registers than BMODE 1's).
 template <int BM, int BN, int WGM, int AMODE, int BMODE, bool SPLIT>
 __global__ __launch_bounds__(kThreads) void k_gemm(GemmArgs g, SplitArgs sp, int tiles_m, int tiles_mn) {
     constexpr int WGN = 4 / WGM;
@@ -177,7 +180,7 @@ __global__ __launch_bounds__(kThreads) void k_gemm(GemmArgs g, SplitArgs sp, int
     constexpr int TA = BM / 4, RA = kThreads / TA, EA = AMODE == 0 ? kBK / RA : BM / (kThreads / (kBK / 4));
     // B dense: float4 along n; B im2col: one column per thread
     constexpr int TB4 = BN / 4, RB4 = kThreads / TB4, EB4 = BMODE == 0 ? kBK / RB4 : 1;
-    constexpr int RB1 = kThreads / BN, EB1 = BMODE == 1 ? kBK / RB1 : 1;
+    constexpr int RB1 = kThreads / BN, EB1 = BMODE >= 1 ? kBK / RB1 : 1;
     constexpr int KH = kBK / 2;  // MFMA k-steps per tile
     static_assert(TM >= 1 && TN >= 1 && EA >= 1 && EB4 >= 1 && EB1 >= 1, "bad tile");
     static_assert(WM % 32 == 0 && WN % 32 == 0, "wave tile must be 32-aligned");
@@ -216,7 +219,7 @@ __global__ __launch_bounds__(kThreads) void k_gemm(GemmArgs g, SplitArgs sp, int
     const int gn1 = n0 + bn1;
     const bool bn_ok = gn1 < N;
     int iy0 = 0, ix0 = 0;
-    if (BMODE == 1) {
+    if (BMODE >= 1) {
         const int oy = gn1 / g.OW, ox = gn1 - oy * g.OW;
         iy0 = oy * g.S - g.P;
         ix0 = ox * g.S - g.P;
@@ -295,7 +298,9 @@ __global__ __launch_bounds__(kThreads) void k_gemm(GemmArgs g, SplitArgs sp, int
     // clamped scalars.
     auto body = [&](auto edge_tag, auto tap_tag) {
         constexpr bool EDGE = decltype(edge_tag)::value;
-        constexpr bool ONE_TAP = decltype(tap_tag)::value;  // im2col with IC % kBK == 0
+        // im2col k tiles: 1 = one tap per tile (IC % kBK == 0, K % kBK == 0),
+        // 2 = at most two taps (IC >= kBK), 0 = generic
+        constexpr int TAPS = decltype(tap_tag)::value;
         auto load = [&](St &r, int kt) {
             const int k0 = kt * kBK;
             if (AMODE == 0) {
@@ -336,11 +341,11 @@ __global__ __launch_bounds__(kThreads) void k_gemm(GemmArgs g, SplitArgs sp, int
                         r.b4[e].w = row[min(gn4 + 3, N - 1)];
                     }
                 }
-            } else if (ONE_TAP) {
-                // the whole k tile is one tap (IC % kBK == 0, K % kBK == 0): one
-                // bounds test per tile, rows RB1 channels apart.  A lane outside
-                // the image reads a clamped in-image address (its value is
-                // masked at the store), not one shared address.
+            } else if (TAPS == 1) {
+                // the whole k tile is one tap: one bounds test and base per
+                // tile, rows RB1 channels apart.  A lane outside the image reads
+                // a clamped in-image address (its value is masked at the store),
+                // not one shared address.
                 const int tap = k0 / g.IC;
                 const int kh = tap / g.KW, kw = tap - kh * g.KW;
                 const int iy = iy0 + kh, ix = ix0 + kw;
@@ -350,6 +355,35 @@ __global__ __launch_bounds__(kThreads) void k_gemm(GemmArgs g, SplitArgs sp, int
 #pragma unroll
                 for (int e = 0; e < EB1; e++) r.b1[e] = B[base + (uint32_t)(e * RB1 * plane)];
                 r.ok1 = ok ? 0xFFFFFFFFu : 0u;
+            } else if (TAPS == 2) {
+                // IC >= kBK: a k tile spans at most two kernel taps, so each
+                // row picks one of two per-tile bases and bounds tests; rows
+                // are RB1 channels apart.  A lane outside the image reads a
+                // clamped in-image address (its value is masked at the store).
+                const int tap0 = k0 / g.IC, ic0 = k0 - tap0 * g.IC;
+                const int ntap = g.K / g.IC;
+                uint32_t base[2];
+                bool okt[2];
+#pragma unroll
+                for (int h = 0; h < 2; h++) {
+                    const int tap = min(tap0 + h, ntap - 1);
+                    const int kh = tap / g.KW, kw = tap - kh * g.KW;
+                    const int iy = iy0 + kh, ix = ix0 + kw;
+                    okt[h] = bn_ok && tap0 + h < ntap && iy >= 0 && iy < g.IH && ix >= 0 && ix < g.IW;
+                    // channel of row r: ic0 + r (tap0) or ic0 + r - IC (tap0 + 1)
+                    base[h] = (uint32_t)((ic0 - h * g.IC) * plane + min(max(iy, 0), g.IH - 1) * g.IW +
+                                         min(max(ix, 0), g.IW - 1));
+                }
+                const int split = g.IC - ic0;  // rows r < split are tap0's
+                uint32_t okm = 0;
+#pragma unroll
+                for (int e = 0; e < EB1; e++) {
+                    const int rr = bk1 + e * RB1;
+                    const bool second = rr >= split;
+                    r.b1[e] = B[(second ? base[1] : base[0]) + (uint32_t)(rr * plane)];
+                    okm |= ((second ? okt[1] : okt[0]) && k0 + rr < K ? 1u : 0u) << e;
+                }
+                r.ok1 = okm;
             } else {
                 // k = (kh*KW + kw)*IC + ic: decompose the first row once, then
                 // step ic by RB1 with carries into kw and kh
@@ -456,17 +490,24 @@ __global__ __launch_bounds__(kThreads) void k_gemm(GemmArgs g, SplitArgs sp, int
     const bool edge_m = AMODE == 0 && m0 + BM > M && (M & 3) != 0;  // row-major A clamps rows itself
     const bool edge_n = BMODE == 0 && n0 + BN > N && g.n_vec == 0;  // im2col B masks per element
     if constexpr (BMODE == 1) {
-        const bool one_tap = g.IC % kBK == 0 && K % kBK == 0;
+        using T0 = std::integral_constant<int, 0>;
+        using T1 = std::integral_constant<int, 1>;
+        const bool one = g.IC % kBK == 0 && K % kBK == 0;
         if (edge_m || edge_n) {
-            if (one_tap) body(std::true_type{}, std::true_type{});
-            else body(std::true_type{}, std::false_type{});
+            if (one) body(std::true_type{}, T1{});
+            else body(std::true_type{}, T0{});
         } else {
-            if (one_tap) body(std::false_type{}, std::true_type{});
-            else body(std::false_type{}, std::false_type{});
+            if (one) body(std::false_type{}, T1{});
+            else body(std::false_type{}, T0{});
         }
+    } else if constexpr (BMODE == 2) {
+        using T2 = std::integral_constant<int, 2>;
+        if (edge_m || edge_n) body(std::true_type{}, T2{});
+        else body(std::false_type{}, T2{});
     } else {
-        if (edge_m || edge_n) body(std::true_type{}, std::false_type{});
-        else body(std::false_type{}, std::false_type{});
+        using T0 = std::integral_constant<int, 0>;
+        if (edge_m || edge_n) body(std::true_type{}, T0{});
+        else body(std::false_type{}, T0{});
     }
 
     gemm_epilogue<TM, TN, SPLIT>(acc, g, sp, split, bz, m0 + wm0, n0 + wn0, lane);
@@ -1103,7 +1144,7 @@ hipError_t launch(const GemmArgs &g, int S, const GemmWorkspace &ws, hipStream_t
     if (total <= 0 || total > 0x7fffffff) return hipErrorInvalidValue;
     // the kernel addresses A and B within one batch plane with 32-bit offsets
     const int64_t a_ext = AMODE == 0 ? (int64_t)g.K * g.lda : (int64_t)g.M * g.lda;
-    const int64_t b_ext = BMODE == 0 ? (int64_t)g.K * g.ldb : (int64_t)g.IC * g.IH * g.IW;
+    const int64_t b_ext = BMODE == 0 ? (int64_t)g.K * g.ldb : (int64_t)g.IC * g.IH * g.IW;  // im2col: the image
     if (a_ext + BM > 0x7fffffff || b_ext + BN > 0x7fffffff) return hipErrorInvalidValue;
     SplitArgs sp{1, 0, nullptr};
     if (S > 1) {
@@ -1181,6 +1222,14 @@ hipError_t dispatch(const GemmArgs &g_in, const GemmWorkspace &ws, hipStream_t s
         if (p.cfg == 5) return launch<32, 128, 1, 1, 0>(g, p.splits, ws, s);
         return launch<64, 64, 2, 1, 0>(g, p.splits, ws, s);
     }
+    if constexpr (BMODE == 1) {
+        // IC >= kBK without one tap per k tile: the two-tap loader (64x64 or
+        // 32x128 blocks, the shapes the im2col planner picks)
+        if (g.IC >= kBK && !(g.IC % kBK == 0 && g.K % kBK == 0)) {
+            if (p.cfg == 5) return launch<32, 128, 1, 0, 2>(g, p.splits, ws, s);
+            if (p.cfg == 3) return launch<64, 64, 2, 0, 2>(g, p.splits, ws, s);
+        }
+    }
     switch (p.cfg) {
         case 0: return launch<128, 128, 2, 0, BMODE>(g, p.splits, ws, s);
         case 1: return launch<64, 128, 2, 0, BMODE>(g, p.splits, ws, s);
@@ -1238,8 +1287,9 @@ std::string gemm_kernel_name(const GemmArgs &g, int64_t ws_bytes, bool im2col) {
         snprintf(buf, sizeof(buf), "k_gemm_dma<%d, %d, %d, %s, 2, %d>%s", bm, bn, wgm, p.splits > 1 ? "true" : "false",
                  kg, p.splits > 1 ? "+k_splitk_reduce" : "");
     } else {
+        const bool two_tap = im2col && g.IC >= kBK && !(g.IC % kBK == 0 && g.K % kBK == 0) && (p.cfg == 3 || p.cfg == 5);
         snprintf(buf, sizeof(buf), "k_gemm<%d, %d, %d, %d, %d, %s>%s", bm, bn, wgm, g.a_rowmajor ? 1 : 0,
-                 im2col ? 1 : 0, p.splits > 1 ? "true" : "false", p.splits > 1 ? "+k_splitk_reduce" : "");
+                 two_tap ? 2 : im2col ? 1 : 0, p.splits > 1 ? "true" : "false", p.splits > 1 ? "+k_splitk_reduce" : "");
     }
     return buf;
 }

@@ -311,9 +311,12 @@ def test_conv_im2col_config3(hip, orc, IC, IH, IW, OC, K, S, P, act):
 
 @pytest.mark.parametrize("IC,IH,IW,OC,K,S,P", [(1, 1, 1, 1, 1, 1, 0), (2, 5, 3, 3, 2, 1, 0), (7, 9, 8, 5, 3, 2, 1),
                                                (16, 33, 31, 70, 3, 2, 1), (4, 6, 6, 9, 5, 1, 2), (3, 2, 2, 4, 3, 1, 1),
-                                               # one tap per k tile (IC % 32 == 0), ragged M / N and borders
+                                               # IC >= 32: at most two taps per k tile, ragged M / N,
+                                               # borders and (IC % 32 != 0) a ragged last k tile
                                                (32, 33, 31, 40, 3, 2, 1), (64, 17, 19, 20, 2, 1, 0),
-                                               (32, 9, 9, 7, 3, 1, 1), (96, 5, 4, 33, 3, 1, 1)])
+                                               (32, 9, 9, 7, 3, 1, 1), (96, 5, 4, 33, 3, 1, 1),
+                                               (40, 11, 13, 12, 3, 1, 1), (33, 9, 8, 5, 2, 1, 0),
+                                               (48, 21, 22, 36, 3, 2, 1)])
 def test_conv_im2col_shapes(hip, orc, IC, IH, IW, OC, K, S, P):
     say(f"im2col conv edge k{K}s{S}p{P} {IC}->{OC} @{IH}x{IW}")
     rng = np.random.default_rng(IC + IH + IW + OC + K)
