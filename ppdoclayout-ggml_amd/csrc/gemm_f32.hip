@@ -166,9 +166,9 @@ __device__ __forceinline__ void gemm_epilogue(const f32x16 (&acc)[TM][TN], const
 
 // AMODE 0: A k-major; AMODE 1: A row-major (K % 4 == 0, lda % 4 == 0).
 // BMODE 0: dense B; BMODE 1: implicit im2col B (generic, or one kernel tap
-// per k tile when IC % kBK == 0); BMODE 2: implicit im2col B with IC >= kBK,
-// at most two taps per k tile (its own instantiation: its loader needs more
-// registers than BMODE 1's).
+// per k tile when IC % kBK == 0); BMODE 2: implicit im2col B with IC >= kBK
+// or IC == kBK / 2, at most two taps per k tile (its own instantiation: its
+// loader needs more registers than BMODE 1's).
 template <int BM, int BN, int WGM, int AMODE, int BMODE, bool SPLIT>
 __global__ __launch_bounds__(kThreads) void k_gemm(GemmArgs g, SplitArgs sp, int tiles_m, int tiles_mn) {
     constexpr int WGN = 4 / WGM;
@@ -356,7 +356,8 @@ __global__ __launch_bounds__(kThreads) void k_gemm(GemmArgs g, SplitArgs sp, int
                 for (int e = 0; e < EB1; e++) r.b1[e] = B[base + (uint32_t)(e * RB1 * plane)];
                 r.ok1 = ok ? 0xFFFFFFFFu : 0u;
             } else if (TAPS == 2) {
-                // IC >= kBK: a k tile spans at most two kernel taps, so each
+                // IC >= kBK, or IC == kBK / 2 (k tiles start on tap
+                // boundaries): a k tile spans at most two kernel taps, so each
                 // row picks one of two per-tile bases and bounds tests; rows
                 // are RB1 channels apart.  A lane outside the image reads a
                 // clamped in-image address (its value is masked at the store).
@@ -1223,9 +1224,10 @@ hipError_t dispatch(const GemmArgs &g_in, const GemmWorkspace &ws, hipStream_t s
         return launch<64, 64, 2, 1, 0>(g, p.splits, ws, s);
     }
     if constexpr (BMODE == 1) {
-        // IC >= kBK without one tap per k tile: the two-tap loader (64x64 or
-        // 32x128 blocks, the shapes the im2col planner picks)
-        if (g.IC >= kBK && !(g.IC % kBK == 0 && g.K % kBK == 0)) {
+        // IC >= kBK without one tap per k tile, or IC == kBK / 2 (every k tile
+        // exactly two taps): the two-tap loader (64x64 or 32x128 blocks, the
+        // shapes the im2col planner picks)
+        if ((g.IC >= kBK && !(g.IC % kBK == 0 && g.K % kBK == 0)) || g.IC == kBK / 2) {
             if (p.cfg == 5) return launch<32, 128, 1, 0, 2>(g, p.splits, ws, s);
             if (p.cfg == 3) return launch<64, 64, 2, 0, 2>(g, p.splits, ws, s);
         }
@@ -1287,7 +1289,8 @@ std::string gemm_kernel_name(const GemmArgs &g, int64_t ws_bytes, bool im2col) {
         snprintf(buf, sizeof(buf), "k_gemm_dma<%d, %d, %d, %s, 2, %d>%s", bm, bn, wgm, p.splits > 1 ? "true" : "false",
                  kg, p.splits > 1 ? "+k_splitk_reduce" : "");
     } else {
-        const bool two_tap = im2col && g.IC >= kBK && !(g.IC % kBK == 0 && g.K % kBK == 0) && (p.cfg == 3 || p.cfg == 5);
+        const bool two_tap = im2col && ((g.IC >= kBK && !(g.IC % kBK == 0 && g.K % kBK == 0)) || g.IC == kBK / 2) &&
+                             (p.cfg == 3 || p.cfg == 5);
         snprintf(buf, sizeof(buf), "k_gemm<%d, %d, %d, %d, %d, %s>%s", bm, bn, wgm, g.a_rowmajor ? 1 : 0,
                  two_tap ? 2 : im2col ? 1 : 0, p.splits > 1 ? "true" : "false", p.splits > 1 ? "+k_splitk_reduce" : "");
     }

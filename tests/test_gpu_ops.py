@@ -316,7 +316,9 @@ def test_conv_im2col_config3(hip, orc, IC, IH, IW, OC, K, S, P, act):
                                                (32, 33, 31, 40, 3, 2, 1), (64, 17, 19, 20, 2, 1, 0),
                                                (32, 9, 9, 7, 3, 1, 1), (96, 5, 4, 33, 3, 1, 1),
                                                (40, 11, 13, 12, 3, 1, 1), (33, 9, 8, 5, 2, 1, 0),
-                                               (48, 21, 22, 36, 3, 2, 1)])
+                                               (48, 21, 22, 36, 3, 2, 1),
+                                               # IC == 16: every k tile exactly two taps
+                                               (16, 17, 15, 32, 2, 1, 0), (16, 9, 10, 20, 3, 2, 1)])
 def test_conv_im2col_shapes(hip, orc, IC, IH, IW, OC, K, S, P):
     say(f"im2col conv edge k{K}s{S}p{P} {IC}->{OC} @{IH}x{IW}")
     rng = np.random.default_rng(IC + IH + IW + OC + K)
