@@ -114,17 +114,26 @@ __global__ __launch_bounds__(256) void k_mask_box(const float *__restrict__ ml,
     if (q >= nq) return;
     const float4 *m4 = reinterpret_cast<const float4 *>(ml + (int64_t)q * kMaskPix);
     int xmin = kMaskHW, xmax = -1, ymin = kMaskHW, ymax = -1;
-    for (int i = threadIdx.x; i < kMaskPix / 4; i += 256) {
-        const float4 v = m4[i];
-        const int y = (4 * i) / kMaskHW, x = 4 * i - y * kMaskHW;  // 200 % 4 == 0: same row
-        const float e[4] = {v.x, v.y, v.z, v.w};
+    // 8 float4 loads in flight per thread and step (indices past the mask
+    // clamped, their values ignored); branch-free integer min / max, exact
+    // in any order
+    constexpr int kN4 = kMaskPix / 4, kU = 8;
+    for (int i0 = threadIdx.x; i0 < kN4; i0 += 256 * kU) {
+        float4 v[kU];
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            if (e[j] > 0.0f) {
-                xmin = min(xmin, x + j);
-                xmax = max(xmax, x + j);
-                ymin = min(ymin, y);
-                ymax = max(ymax, y);
+        for (int u = 0; u < kU; u++) v[u] = m4[min(i0 + u * 256, kN4 - 1)];
+#pragma unroll
+        for (int u = 0; u < kU; u++) {
+            const int i = i0 + u * 256;
+            const int y = (4 * i) / kMaskHW, x = 4 * i - y * kMaskHW;  // 200 % 4 == 0: same row
+            const float e[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const bool pos = i < kN4 && e[j] > 0.0f;
+                xmin = min(xmin, pos ? x + j : kMaskHW);
+                xmax = max(xmax, pos ? x + j : -1);
+                ymin = min(ymin, pos ? y : kMaskHW);
+                ymax = max(ymax, pos ? y : -1);
             }
         }
     }

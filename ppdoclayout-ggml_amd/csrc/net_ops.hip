@@ -79,9 +79,55 @@ __global__ __launch_bounds__(256) void k_maxpool2_padend(const float *__restrict
     out[idx] = fmaxf(fmaxf(v00, v01), fmaxf(v10, v11));
 }
 
+// The same pool, four outputs per thread (W % 4 == 0, 16-byte aligned planes:
+// checked on the host): two aligned float4 row loads plus the next column of
+// each row, one float4 store.  Same max order as k_maxpool2_padend.
+__global__ __launch_bounds__(256) void k_maxpool2_padend4(const float *__restrict__ x, float *__restrict__ out,
+                                                          int C, int H, int W) {
+    const int W4 = W / 4;
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= (int64_t)C * H * W4) return;
+    const int c = (int)(idx / ((int64_t)H * W4));
+    const int rem = (int)(idx - (int64_t)c * H * W4);
+    const int y = rem / W4, x0 = 4 * (rem - y * W4);
+    const float *r0 = x + ((int64_t)c * H + y) * W + x0;
+    const bool down = y + 1 < H, right = x0 + 4 < W;
+    const float *r1 = down ? r0 + W : r0;
+    const float4 a = *reinterpret_cast<const float4 *>(r0), b = *reinterpret_cast<const float4 *>(r1);
+    const float a4 = right ? r0[4] : 0.0f, b4 = (right && down) ? r1[4] : 0.0f;
+    const float bx = down ? b.x : 0.0f, by = down ? b.y : 0.0f, bz = down ? b.z : 0.0f, bw = down ? b.w : 0.0f;
+    float4 o;
+    o.x = fmaxf(fmaxf(a.x, a.y), fmaxf(bx, by));
+    o.y = fmaxf(fmaxf(a.y, a.z), fmaxf(by, bz));
+    o.z = fmaxf(fmaxf(a.z, a.w), fmaxf(bz, bw));
+    o.w = fmaxf(fmaxf(a.w, a4), fmaxf(bw, b4));
+    *reinterpret_cast<float4 *>(out + ((int64_t)c * H + y) * W + x0) = o;
+}
+
 // Interpolation (ggml_interpolate, src/ppdoclayout.cpp:670-672): nearest
 // (src = floor(dst * in / out)) or bilinear with half-pixel centres and
 // edge clamping; out = interp(x) + add (add may be null).
+__device__ __forceinline__ float interp_at(const float *__restrict__ xc, int IH, int IW, int OH, int OW, int oy,
+                                           int ox, int bilinear) {
+    if (!bilinear) {
+        const int iy = (int)((int64_t)oy * IH / OH), ix = (int)((int64_t)ox * IW / OW);
+        return xc[(int64_t)iy * IW + ix];
+    }
+    const float sy = (float)OH / (float)IH, sx = (float)OW / (float)IW;
+    const float fy = ((float)oy + 0.5f) / sy - 0.5f, fx = ((float)ox + 0.5f) / sx - 0.5f;
+    const float fly = floorf(fy), flx = floorf(fx);
+    int y0 = (int)fly, x0 = (int)flx;
+    int y1 = y0 + 1, x1 = x0 + 1;
+    y0 = max(0, min(y0, IH - 1));
+    y1 = max(0, min(y1, IH - 1));
+    x0 = max(0, min(x0, IW - 1));
+    x1 = max(0, min(x1, IW - 1));
+    const float dy = fmaxf(0.0f, fminf(fy - fly, 1.0f)), dx = fmaxf(0.0f, fminf(fx - flx, 1.0f));
+    const float a = xc[(int64_t)y0 * IW + x0], bb = xc[(int64_t)y0 * IW + x1];
+    const float cc = xc[(int64_t)y1 * IW + x0], d = xc[(int64_t)y1 * IW + x1];
+    return a * (1.0f - dx) * (1.0f - dy) + bb * dx * (1.0f - dy) + cc * (1.0f - dx) * dy + d * dx * dy;
+}
+
 __global__ __launch_bounds__(256) void k_interp(const float *__restrict__ x, const float *__restrict__ add,
                                                 float *__restrict__ out, int C, int IH, int IW, int OH, int OW,
                                                 int bilinear) {
@@ -90,28 +136,36 @@ __global__ __launch_bounds__(256) void k_interp(const float *__restrict__ x, con
     const int c = (int)(idx / ((int64_t)OH * OW));
     const int rem = (int)(idx - (int64_t)c * OH * OW);
     const int oy = rem / OW, ox = rem - oy * OW;
-    const float *xc = x + (int64_t)c * IH * IW;
-    float v;
-    if (!bilinear) {
-        const int iy = (int)((int64_t)oy * IH / OH), ix = (int)((int64_t)ox * IW / OW);
-        v = xc[(int64_t)iy * IW + ix];
-    } else {
-        const float sy = (float)OH / (float)IH, sx = (float)OW / (float)IW;
-        const float fy = ((float)oy + 0.5f) / sy - 0.5f, fx = ((float)ox + 0.5f) / sx - 0.5f;
-        const float fly = floorf(fy), flx = floorf(fx);
-        int y0 = (int)fly, x0 = (int)flx;
-        int y1 = y0 + 1, x1 = x0 + 1;
-        y0 = max(0, min(y0, IH - 1));
-        y1 = max(0, min(y1, IH - 1));
-        x0 = max(0, min(x0, IW - 1));
-        x1 = max(0, min(x1, IW - 1));
-        const float dy = fmaxf(0.0f, fminf(fy - fly, 1.0f)), dx = fmaxf(0.0f, fminf(fx - flx, 1.0f));
-        const float a = xc[(int64_t)y0 * IW + x0], bb = xc[(int64_t)y0 * IW + x1];
-        const float cc = xc[(int64_t)y1 * IW + x0], d = xc[(int64_t)y1 * IW + x1];
-        v = a * (1.0f - dx) * (1.0f - dy) + bb * dx * (1.0f - dy) + cc * (1.0f - dx) * dy + d * dx * dy;
-    }
+    float v = interp_at(x + (int64_t)c * IH * IW, IH, IW, OH, OW, oy, ox, bilinear);
     if (add) v += add[idx];
     out[idx] = v;
+}
+
+// Four consecutive outputs per thread (OW % 4 == 0, 16-byte aligned out /
+// add: checked on the host), one float4 store; same values as k_interp.
+__global__ __launch_bounds__(256) void k_interp4(const float *__restrict__ x, const float *__restrict__ add,
+                                                 float *__restrict__ out, int C, int IH, int IW, int OH, int OW,
+                                                 int bilinear) {
+    const int OW4 = OW / 4;
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= (int64_t)C * OH * OW4) return;
+    const int c = (int)(idx / ((int64_t)OH * OW4));
+    const int rem = (int)(idx - (int64_t)c * OH * OW4);
+    const int oy = rem / OW4, ox = 4 * (rem - oy * OW4);
+    const float *xc = x + (int64_t)c * IH * IW;
+    float4 v = make_float4(interp_at(xc, IH, IW, OH, OW, oy, ox, bilinear),
+                           interp_at(xc, IH, IW, OH, OW, oy, ox + 1, bilinear),
+                           interp_at(xc, IH, IW, OH, OW, oy, ox + 2, bilinear),
+                           interp_at(xc, IH, IW, OH, OW, oy, ox + 3, bilinear));
+    const int64_t o = ((int64_t)c * OH + oy) * OW + ox;
+    if (add) {
+        const float4 a = *reinterpret_cast<const float4 *>(add + o);
+        v.x += a.x;
+        v.y += a.y;
+        v.z += a.z;
+        v.w += a.w;
+    }
+    *reinterpret_cast<float4 *>(out + o) = v;
 }
 
 // ---------------------------------------------------------------------------
@@ -149,14 +203,15 @@ __global__ __launch_bounds__(256) void k_layernorm(const float *__restrict__ a, 
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) q += __shfl_xor(q, o);
     const float scale = 1.0f / sqrtf(q / (float)kDM + eps);
+    const float4 gv = *reinterpret_cast<const float4 *>(gamma + lane * 4);
+    const float4 bv = *reinterpret_cast<const float4 *>(beta + lane * 4);
+    const float y[4] = {v[0] * scale * gv.x + bv.x, v[1] * scale * gv.y + bv.y, v[2] * scale * gv.z + bv.z,
+                        v[3] * scale * gv.w + bv.w};
+    if (out_chw) {
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int c = lane * 4 + i;
-        const float y = v[i] * scale * gamma[c] + beta[c];
-        if (out_chw)
-            out[(int64_t)c * T + t] = y;
-        else
-            out[(int64_t)t * kDM + c] = y;
+        for (int i = 0; i < 4; i++) out[(int64_t)(lane * 4 + i) * T + t] = y[i];
+    } else {
+        *reinterpret_cast<float4 *>(out + (int64_t)t * kDM + lane * 4) = make_float4(y[0], y[1], y[2], y[3]);
     }
 }
 
@@ -381,12 +436,21 @@ hipError_t dwconv(const float *x, const float *w, const float *b, float *out, in
 }
 
 hipError_t maxpool2_padend(const float *x, float *out, int C, int H, int W, hipStream_t s) {
-    hipLaunchKernelGGL(k_maxpool2_padend, dim3(blocks_for((int64_t)C * H * W)), dim3(256), 0, s, x, out, C, H, W);
+    if (W % 4 == 0 && (((uintptr_t)x | (uintptr_t)out) & 15) == 0)
+        hipLaunchKernelGGL(k_maxpool2_padend4, dim3(blocks_for((int64_t)C * H * (W / 4))), dim3(256), 0, s, x, out, C,
+                           H, W);
+    else
+        hipLaunchKernelGGL(k_maxpool2_padend, dim3(blocks_for((int64_t)C * H * W)), dim3(256), 0, s, x, out, C, H, W);
     return hipGetLastError();
 }
 
 hipError_t interp(const float *x, const float *add, float *out, int C, int IH, int IW, int OH, int OW,
                   int bilinear, hipStream_t s) {
+    if (OW % 4 == 0 && (((uintptr_t)out | (uintptr_t)add) & 15) == 0) {
+        hipLaunchKernelGGL(k_interp4, dim3(blocks_for((int64_t)C * OH * (OW / 4))), dim3(256), 0, s, x, add, out, C,
+                           IH, IW, OH, OW, bilinear);
+        return hipGetLastError();
+    }
     hipLaunchKernelGGL(k_interp, dim3(blocks_for((int64_t)C * OH * OW)), dim3(256), 0, s, x, add, out, C, IH, IW,
                        OH, OW, bilinear);
     return hipGetLastError();
@@ -394,6 +458,9 @@ hipError_t interp(const float *x, const float *add, float *out, int C, int IH, i
 
 hipError_t layernorm(const float *a, const float *b, const float *gamma, const float *beta, float *out, int T,
                      int out_chw, hipStream_t s) {
+    // rows, gamma, beta and (token-major) out are accessed as float4
+    if ((((uintptr_t)a | (uintptr_t)b | (uintptr_t)gamma | (uintptr_t)beta | (uintptr_t)out) & 15) != 0)
+        return hipErrorInvalidValue;
     hipLaunchKernelGGL(k_layernorm, dim3((T + 3) / 4), dim3(256), 0, s, a, b, gamma, beta, out, T, 1e-5f, out_chw);
     return hipGetLastError();
 }
