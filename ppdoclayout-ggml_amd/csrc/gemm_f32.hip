@@ -78,8 +78,9 @@ struct Stage {
 // Epilogue of a wave's (32 TM) x (32 TN) accumulator tile whose top-left
 // output is (mw, nw): split-K partials, or bias / residual add / act and the
 // store in C's layout.  32x32 accumulator layout: lane owns column (lane & 31)
-// and rows 8*(r/4) + 4*(lane/32) + r%4 of register r.
-template <int TM, int TN, bool SPLIT>
+// and rows 8*(r/4) + 4*(lane/32) + r%4 of register r.  Only registers
+// r in [RB, RB + RN) are stored (RB, RN multiples of 4).
+template <int TM, int TN, bool SPLIT, int RB = 0, int RN = 16>
 __device__ __forceinline__ void gemm_epilogue(const f32x16 (&acc)[TM][TN], const GemmArgs &g, const SplitArgs &sp,
                                               int split, int bz, int mw, int nw, int lane) {
     const int M = g.M, N = g.N, l32 = lane & 31;
@@ -92,7 +93,7 @@ __device__ __forceinline__ void gemm_epilogue(const f32x16 (&acc)[TM][TN], const
 #pragma unroll
                 for (int i = 0; i < TM; i++)
 #pragma unroll
-                    for (int r = 0; r < 16; r++) {
+                    for (int r = RB; r < RB + RN; r++) {
                         const int m = mw + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
                         if (m < M) P[(int64_t)m * N + n] = acc[i][j][r];
                     }
@@ -121,7 +122,7 @@ __device__ __forceinline__ void gemm_epilogue(const f32x16 (&acc)[TM][TN], const
 #pragma unroll
                 for (int i = 0; i < TM; i++) {
 #pragma unroll
-                    for (int r = 0; r < 16; r++) {
+                    for (int r = RB; r < RB + RN; r++) {
                         const int m = mw + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
                         if (m < M) {
                             const int64_t idx = (int64_t)m * g.ldc + n;
@@ -142,7 +143,7 @@ __device__ __forceinline__ void gemm_epilogue(const f32x16 (&acc)[TM][TN], const
 #pragma unroll
                 for (int i = 0; i < TM; i++) {
 #pragma unroll
-                    for (int q = 0; q < 4; q++) {
+                    for (int q = RB / 4; q < (RB + RN) / 4; q++) {
                         const int mb = mw + i * 32 + 8 * q + 4 * (lane >> 5);
                         const int64_t idx = (int64_t)n * g.ldc + mb;
                         if (vec_ok && mb + 3 < M) {
@@ -688,26 +689,49 @@ __global__ __launch_bounds__(kThreads * KG) void k_gemm_dma(GemmArgs g, SplitArg
         wait_vmcnt<0>();  // no copy may still target this block's LDS when it exits
     }
     if constexpr (KG == 2) {
-        // group 1's partial tile joins group 0's through the (now idle) stages
-        static_assert(4 * TM * TN * 16 * 64 <= NS * (SA + SB), "reduction space");
+        // The groups' partial tiles are summed through the (now idle) stages
+        // and each group finishes half of the rows: group 0 registers 0-7,
+        // group 1 registers 8-15 (the same sums as one group adding the
+        // other's whole tile; the epilogue's stores split across 8 waves).
+        constexpr int HALF = TM * TN * 8 * 64;  // floats one wave hands over
+        static_assert(2 * 4 * HALF <= NS * (SA + SB), "reduction space");
         __syncthreads();  // every wave's last compute() has read its operands
-        float *red = smem + wq * (TM * TN * 16 * 64) + lane;
-        if (grp == 1) {
+        float *give = smem + (grp * 4 + wq) * HALF + lane;
+        const float *take = smem + ((1 - grp) * 4 + wq) * HALF + lane;
+        if (grp == 0) {
 #pragma unroll
             for (int i = 0; i < TM; i++)
 #pragma unroll
                 for (int j = 0; j < TN; j++)
 #pragma unroll
-                    for (int r = 0; r < 16; r++) red[((i * TN + j) * 16 + r) * 64] = acc[i][j][r];
+                    for (int r = 0; r < 8; r++) give[((i * TN + j) * 8 + r) * 64] = acc[i][j][8 + r];
+        } else {
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int j = 0; j < TN; j++)
+#pragma unroll
+                    for (int r = 0; r < 8; r++) give[((i * TN + j) * 8 + r) * 64] = acc[i][j][r];
         }
         __syncthreads();
-        if (grp == 1) return;
+        if (grp == 0) {
 #pragma unroll
-        for (int i = 0; i < TM; i++)
+            for (int i = 0; i < TM; i++)
 #pragma unroll
-            for (int j = 0; j < TN; j++)
+                for (int j = 0; j < TN; j++)
 #pragma unroll
-                for (int r = 0; r < 16; r++) acc[i][j][r] += red[((i * TN + j) * 16 + r) * 64];
+                    for (int r = 0; r < 8; r++) acc[i][j][r] += take[((i * TN + j) * 8 + r) * 64];
+            gemm_epilogue<TM, TN, SPLIT, 0, 8>(acc, g, sp, split, bz, m0 + wm0, n0 + wn0, lane);
+        } else {
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int j = 0; j < TN; j++)
+#pragma unroll
+                    for (int r = 0; r < 8; r++) acc[i][j][8 + r] += take[((i * TN + j) * 8 + r) * 64];
+            gemm_epilogue<TM, TN, SPLIT, 8, 8>(acc, g, sp, split, bz, m0 + wm0, n0 + wn0, lane);
+        }
+        return;
     }
     gemm_epilogue<TM, TN, SPLIT>(acc, g, sp, split, bz, m0 + wm0, n0 + wn0, lane);
 }
@@ -1072,8 +1096,10 @@ GemmPlan plan_auto(int M, int N, int K, int batch, bool im2col) {
     GemmPlan p{M <= 32 ? 5 : 3, 1};
     const int nk = (K + kBK - 1) / kBK;
     const int64_t tiles = tiles_of(p.cfg, M, N, batch);
-    int64_t want = 1000 / (tiles > 0 ? tiles : 1);
-    const int64_t cap = nk / 6;
+    static const int64_t target = env_int("PPDL_SPLIT_BLOCKS", 1000);
+    static const int64_t min_kt = env_int("PPDL_SPLIT_MIN_KT", 6);
+    int64_t want = target / (tiles > 0 ? tiles : 1);
+    const int64_t cap = nk / min_kt;
     if (want > cap) want = cap;
     for (int S : kSplitChoices)
         if (S <= want) p.splits = S;
