@@ -80,9 +80,32 @@ struct Stage {
 // store in C's layout.  32x32 accumulator layout: lane owns column (lane & 31)
 // and rows 8*(r/4) + 4*(lane/32) + r%4 of register r.  Only registers
 // r in [RB, RB + RN) are stored (RB, RN multiples of 4).
-template <int TM, int TN, bool SPLIT, int RB = 0, int RN = 16>
+//
+// A per-row bias (bias_n == 0) may come pre-loaded in registers (PB, from
+// load_row_bias before the k loop, so its load latency hides under the
+// MFMAs): bv[i][r - RB] is the bias of row m of register r of tile row i.
+template <int TM, int RN>
+struct RowBias {
+    float v[TM][RN];
+};
+
+// rows of registers rb .. rb + RN - 1 (rb a multiple of 4; register rb + r
+// holds the row of register r plus 2 * rb)
+template <int TM, int RN>
+__device__ __forceinline__ void load_row_bias(RowBias<TM, RN> &bv, const GemmArgs &g, int mw, int rb, int lane) {
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int r = 0; r < RN; r++) {
+            const int m = mw + 2 * rb + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            bv.v[i][r] = g.bias[min(m, g.M - 1)];
+        }
+}
+
+template <int TM, int TN, bool SPLIT, int RB = 0, int RN = 16, bool PB = false>
 __device__ __forceinline__ void gemm_epilogue(const f32x16 (&acc)[TM][TN], const GemmArgs &g, const SplitArgs &sp,
-                                              int split, int bz, int mw, int nw, int lane) {
+                                              int split, int bz, int mw, int nw, int lane,
+                                              const RowBias<TM, RN> *bv = nullptr) {
     const int M = g.M, N = g.N, l32 = lane & 31;
     if (SPLIT) {
         float *__restrict__ P = sp.partials + ((int64_t)split * g.batch + bz) * M * N;
@@ -106,8 +129,13 @@ __device__ __forceinline__ void gemm_epilogue(const f32x16 (&acc)[TM][TN], const
     const int act = g.act, add_mode = g.add_mode, bias_n = g.bias_n;
     float *__restrict__ C = g.C + (int64_t)bz * g.sC;
     const float *__restrict__ Ad = g.add ? g.add + (int64_t)bz * g.sC : nullptr;
-    auto epi = [&](float v, int m, int n, int64_t idx) {
-        if (bias) v += bias[bias_n ? n : m];
+    // bias of (m, n) for tile row i, register r (PB: the pre-loaded value)
+    auto bias_of = [&](int i, int r, int m, int n) -> float {
+        if (PB && !bias_n) return bv->v[i][r - RB];
+        return bias[bias_n ? n : m];
+    };
+    auto epi = [&](float v, float bval, int64_t idx) {
+        if (bias) v += bval;
         if (add_mode == 1) v += Ad[idx];
         v = act_f(v, act);
         if (add_mode == 2) v += Ad[idx];
@@ -126,7 +154,7 @@ __device__ __forceinline__ void gemm_epilogue(const f32x16 (&acc)[TM][TN], const
                         const int m = mw + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
                         if (m < M) {
                             const int64_t idx = (int64_t)m * g.ldc + n;
-                            C[idx] = epi(acc[i][j][r], m, n, idx);
+                            C[idx] = epi(acc[i][j][r], bias ? bias_of(i, r, m, n) : 0.0f, idx);
                         }
                     }
                 }
@@ -148,15 +176,17 @@ __device__ __forceinline__ void gemm_epilogue(const f32x16 (&acc)[TM][TN], const
                         const int64_t idx = (int64_t)n * g.ldc + mb;
                         if (vec_ok && mb + 3 < M) {
                             float4 v;
-                            v.x = epi(acc[i][j][4 * q + 0], mb + 0, n, idx + 0);
-                            v.y = epi(acc[i][j][4 * q + 1], mb + 1, n, idx + 1);
-                            v.z = epi(acc[i][j][4 * q + 2], mb + 2, n, idx + 2);
-                            v.w = epi(acc[i][j][4 * q + 3], mb + 3, n, idx + 3);
+                            v.x = epi(acc[i][j][4 * q + 0], bias ? bias_of(i, 4 * q + 0, mb + 0, n) : 0.0f, idx + 0);
+                            v.y = epi(acc[i][j][4 * q + 1], bias ? bias_of(i, 4 * q + 1, mb + 1, n) : 0.0f, idx + 1);
+                            v.z = epi(acc[i][j][4 * q + 2], bias ? bias_of(i, 4 * q + 2, mb + 2, n) : 0.0f, idx + 2);
+                            v.w = epi(acc[i][j][4 * q + 3], bias ? bias_of(i, 4 * q + 3, mb + 3, n) : 0.0f, idx + 3);
                             *reinterpret_cast<float4 *>(C + idx) = v;
                         } else {
 #pragma unroll
                             for (int u = 0; u < 4; u++)
-                                if (mb + u < M) C[idx + u] = epi(acc[i][j][4 * q + u], mb + u, n, idx + u);
+                                if (mb + u < M)
+                                    C[idx + u] = epi(acc[i][j][4 * q + u], bias ? bias_of(i, 4 * q + u, mb + u, n) : 0.0f,
+                                                     idx + u);
                         }
                     }
                 }
@@ -668,6 +698,15 @@ __global__ __launch_bounds__(kThreads * KG) void k_gemm_dma(GemmArgs g, SplitArg
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[q][i], fb[q][j], acc[i][j], 0, 0, 0);
     };
 
+    // The rows' bias (per-row bias, direct store) is loaded before the k loop:
+    // the first tile's wait covers it, and the epilogue does not start with a
+    // memory round trip.  Group g of KG = 2 stores registers 8g .. 8g + 7.
+    constexpr int ERN = KG == 2 ? 8 : 16;
+    const int erb = KG == 2 ? 8 * grp : 0;
+    RowBias<TM, ERN> bv;
+    const bool pre_bias = !SPLIT && g.bias && !g.bias_n;
+    if (pre_bias) load_row_bias(bv, g, m0 + wm0, erb, lane);
+
     if (nk > 0) {
         const int klast = kt1 - 1;
         const int ktail = K - (nk_total - 1) * kBK;  // valid rows of the global last tile
@@ -683,7 +722,12 @@ __global__ __launch_bounds__(kThreads * KG) void k_gemm_dma(GemmArgs g, SplitArg
                 for (int x = tid; x < (kBK - ktail) * BM; x += NT) As[u * SA + ktail * BM + x] = 0.0f;
                 __syncthreads();
             }
-            issue((i + NS - 1) % NS, min(kt + NS - 1, klast));  // into tile kt-1's stage
+            // into tile kt-1's stage.  With two stages the wait above is
+            // vmcnt(0), so the copy past the last tile is simply not issued
+            // (the block would otherwise wait for it before its epilogue);
+            // deeper pipelines keep a fixed copy count per trip for their
+            // vmcnt accounting and repeat the last tile instead.
+            if (NS > 2 || i + 1 < nk) issue((i + NS - 1) % NS, min(kt + NS - 1, klast));
             compute(u);
         }
         wait_vmcnt<0>();  // no copy may still target this block's LDS when it exits
@@ -721,7 +765,11 @@ __global__ __launch_bounds__(kThreads * KG) void k_gemm_dma(GemmArgs g, SplitArg
                 for (int j = 0; j < TN; j++)
 #pragma unroll
                     for (int r = 0; r < 8; r++) acc[i][j][r] += take[((i * TN + j) * 8 + r) * 64];
-            gemm_epilogue<TM, TN, SPLIT, 0, 8>(acc, g, sp, split, bz, m0 + wm0, n0 + wn0, lane);
+            if (pre_bias) {
+                gemm_epilogue<TM, TN, SPLIT, 0, 8, true>(acc, g, sp, split, bz, m0 + wm0, n0 + wn0, lane, &bv);
+            } else {
+                gemm_epilogue<TM, TN, SPLIT, 0, 8>(acc, g, sp, split, bz, m0 + wm0, n0 + wn0, lane);
+            }
         } else {
 #pragma unroll
             for (int i = 0; i < TM; i++)
@@ -729,11 +777,19 @@ __global__ __launch_bounds__(kThreads * KG) void k_gemm_dma(GemmArgs g, SplitArg
                 for (int j = 0; j < TN; j++)
 #pragma unroll
                     for (int r = 0; r < 8; r++) acc[i][j][8 + r] += take[((i * TN + j) * 8 + r) * 64];
-            gemm_epilogue<TM, TN, SPLIT, 8, 8>(acc, g, sp, split, bz, m0 + wm0, n0 + wn0, lane);
+            if (pre_bias) {
+                gemm_epilogue<TM, TN, SPLIT, 8, 8, true>(acc, g, sp, split, bz, m0 + wm0, n0 + wn0, lane, &bv);
+            } else {
+                gemm_epilogue<TM, TN, SPLIT, 8, 8>(acc, g, sp, split, bz, m0 + wm0, n0 + wn0, lane);
+            }
         }
         return;
+    } else {
+        if (pre_bias)
+            gemm_epilogue<TM, TN, SPLIT, 0, 16, true>(acc, g, sp, split, bz, m0 + wm0, n0 + wn0, lane, &bv);
+        else
+            gemm_epilogue<TM, TN, SPLIT>(acc, g, sp, split, bz, m0 + wm0, n0 + wn0, lane);
     }
-    gemm_epilogue<TM, TN, SPLIT>(acc, g, sp, split, bz, m0 + wm0, n0 + wn0, lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -863,6 +919,142 @@ hipError_t launch_patch(const GemmArgs &g, int cc, hipStream_t s) {
         hipLaunchKernelGGL((k_conv_patch<3, 2>), dim3((unsigned)blocks), dim3(kThreads), 0, s, g, cc, nseg);
     else
         hipLaunchKernelGGL((k_conv_patch<2, 1>), dim3((unsigned)blocks), dim3(kThreads), 0, s, g, cc, nseg);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Implicit-im2col conv for at most 32 output channels, operands fetched from
+// global memory straight into MFMA operand registers: no LDS staging and no
+// barrier in the k loop.  A wave owns the (padded) 32 output channels of 32
+// consecutive output pixels; lane l supplies pixel (l & 31) and k slot
+// (l >> 5) of every 32x32x2 step.  The k range is walked tap by tap, two
+// input channels per step: step s of tap t contracts channels 2s and 2s + 1
+// of that tap (k = t*IC + 2s + slot, the .wr row order), so a lane tests its
+// pixel's bounds and forms its base address once per tap.  With odd IC the
+// last step of a tap has a zero second slot in A and B.  A lane issues the
+// loads of kFragU steps before their MFMAs (unconditional, at clamped
+// addresses; the masks are applied to the values).  WV waves of a block take
+// consecutive parts of the step range for the same 32 pixels and add their
+// tiles through LDS in wave order, so the sum order is fixed.
+constexpr int kFragU = 16;
+
+template <int WV>
+__global__ __launch_bounds__(64 * WV) void k_conv_frag(GemmArgs g) {
+    __shared__ float red[WV > 1 ? (WV - 1) * 16 * 64 : 1];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int l32 = lane & 31, slot = lane >> 5;
+    const int grp = xcd_remap(blockIdx.x, gridDim.x);
+    const int M = g.M, N = g.N, IC = g.IC, IH = g.IH, IW = g.IW, KW = g.KW;
+    const int n = grp * 32 + l32;
+    const bool n_ok = n < N;
+    const int nc = n_ok ? n : N - 1;
+    const int oy = nc / g.OW, ox = nc - oy * g.OW;
+    const int iy0 = oy * g.S - g.P, ix0 = ox * g.S - g.P;
+    const int ntap = KW * KW, spt = (IC + 1) >> 1;  // taps, steps per tap
+    const int nsteps = ntap * spt;
+    const int per = (nsteps + WV - 1) / WV;
+    const int j0 = min(nsteps, wave * per), j1 = min(nsteps, j0 + per);
+    const uint32_t plane = (uint32_t)IH * (uint32_t)IW;
+    const float *__restrict__ X = g.B;
+    const float *__restrict__ Wt = g.A;
+    const uint32_t lda = (uint32_t)g.lda;
+    const bool m_ok = l32 < M;
+    const uint32_t mc = (uint32_t)min(l32, M - 1);
+
+    f32x16 acc;
+#pragma unroll
+    for (int r = 0; r < 16; r++) acc[r] = 0.0f;
+
+    // state of the next step: its tap, its step within the tap, and this
+    // lane's bounds test and (clamped) input offset for that tap
+    int tap = j0 / spt, st = j0 - tap * spt;
+    bool in_tap = false;
+    uint32_t xb = 0;
+    auto enter_tap = [&]() {
+        const int t = min(tap, ntap - 1);
+        const int kh = t / KW, kw = t - kh * KW;
+        const int iy = iy0 + kh, ix = ix0 + kw;
+        in_tap = n_ok && tap < ntap && iy >= 0 && iy < IH && ix >= 0 && ix < IW;
+        xb = (uint32_t)(min(max(iy, 0), IH - 1) * IW + min(max(ix, 0), IW - 1));
+    };
+    enter_tap();
+    for (int j = j0; j < j1; j += kFragU) {
+        float av[kFragU], bv[kFragU];
+        bool oka[kFragU], okb[kFragU];
+#pragma unroll
+        for (int u = 0; u < kFragU; u++) {
+            const bool live = j + u < j1;  // wave-uniform
+            const int ic = 2 * st + slot;
+            const uint32_t icc = (uint32_t)min(ic, IC - 1);
+            const uint32_t tc = (uint32_t)min(tap, ntap - 1);
+            bv[u] = X[icc * plane + xb];
+            av[u] = Wt[(tc * (uint32_t)IC + icc) * lda + mc];
+            oka[u] = live && ic < IC && m_ok;
+            okb[u] = live && ic < IC && in_tap;
+            if (live && ++st == spt) {  // wave-uniform
+                st = 0;
+                ++tap;
+                enter_tap();
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kFragU; u++)
+            if (j + u < j1)
+                acc = __builtin_amdgcn_mfma_f32_32x32x2f32(oka[u] ? av[u] : 0.0f, okb[u] ? bv[u] : 0.0f, acc, 0, 0, 0);
+    }
+
+    if constexpr (WV > 1) {
+        if (wave > 0)
+#pragma unroll
+            for (int r = 0; r < 16; r++) red[((wave - 1) * 16 + r) * 64 + lane] = acc[r];
+        __syncthreads();
+        if (wave > 0) return;
+        for (int w = 1; w < WV; w++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[r] += red[((w - 1) * 16 + r) * 64 + lane];
+    }
+    if (!n_ok) return;
+    float *__restrict__ C = g.C;
+    const uint32_t ldc = (uint32_t)g.ldc;
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+        const int m = 8 * (r >> 2) + 4 * slot + (r & 3);
+        if (m < M) C[(uint32_t)m * ldc + (uint32_t)n] = act_f(acc[r] + (g.bias ? g.bias[m] : 0.0f), g.act);
+    }
+}
+
+// The fragment kernel serves op 16 with at most 32 output channels (the stem
+// convs), plain bias + act into a CHW output.  PPDL_CONV_FRAG=0 turns it off.
+bool frag_ok(const GemmArgs &g) {
+    static const bool off = [] {
+        const char *e = getenv("PPDL_CONV_FRAG");
+        return e && e[0] == '0';
+    }();
+    return !off && g.M >= 1 && g.M <= 32 && !g.a_rowmajor && !g.c_trans && g.add_mode == 0 && !g.add &&
+           g.batch == 1 && g.IC >= 1 && g.N >= 1 && (int64_t)g.IC * g.IH * g.IW < (1LL << 31) &&
+           ((int64_t)g.KW * g.KW * g.IC * g.lda + 32) < (1LL << 31) && (int64_t)32 * g.ldc + g.N < (1LL << 31);
+}
+
+// waves per 32-pixel group: about 32 steps per wave, within ~8 resident
+// waves per SIMD over the whole grid
+int frag_waves(const GemmArgs &g) {
+    const int64_t groups = (g.N + 31) / 32;
+    const int64_t nsteps = (int64_t)g.KW * g.KW * ((g.IC + 1) / 2);
+    int wv = 1;
+    while (wv < 8 && nsteps > 32 * wv && groups * wv * 2 <= 8192) wv *= 2;
+    return wv;
+}
+
+hipError_t launch_frag(const GemmArgs &g, hipStream_t s) {
+    const int64_t groups = (g.N + 31) / 32;
+    if (groups > 0x7fffffff) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)groups);
+    switch (frag_waves(g)) {
+        case 1: hipLaunchKernelGGL(k_conv_frag<1>, grid, dim3(64), 0, s, g); break;
+        case 2: hipLaunchKernelGGL(k_conv_frag<2>, grid, dim3(128), 0, s, g); break;
+        case 4: hipLaunchKernelGGL(k_conv_frag<4>, grid, dim3(256), 0, s, g); break;
+        default: hipLaunchKernelGGL(k_conv_frag<8>, grid, dim3(512), 0, s, g); break;
+    }
     return hipGetLastError();
 }
 
@@ -1231,8 +1423,10 @@ template <int BMODE>
 hipError_t dispatch(const GemmArgs &g_in, const GemmWorkspace &ws, hipStream_t s) {
     GemmArgs g = g_in;
     g.n_vec = BMODE == 0 ? n_vec_of(g) : 0;
-    if (BMODE == 1)
+    if (BMODE == 1) {
         if (const int cc = patch_cc(g)) return launch_patch(g, cc, s);
+        if (frag_ok(g)) return launch_frag(g, s);
+    }
     const GemmPlan p = gemm_plan(g, ws.bytes, BMODE == 1);
     if (g.a_add && (BMODE != 0 || !g.a_rowmajor || (((uintptr_t)g.a_add) & 15) != 0 || g.a_add_n % 32 != 0))
         return hipErrorInvalidValue;
@@ -1295,6 +1489,7 @@ GemmPlan gemm_plan(const GemmArgs &g, int64_t ws_bytes, bool im2col) {
 }
 
 int64_t gemm_ws_bytes_for(const GemmArgs &g, bool im2col) {
+    if (im2col && !patch_cc(g) && frag_ok(g)) return 0;  // the fragment kernel splits K inside a block
     const GemmPlan p = gemm_plan(g, INT64_MAX, im2col);
     return gemm_ws_bytes(g.M, g.N, g.batch, p.cfg, p.splits);
 }
@@ -1303,6 +1498,7 @@ hipError_t gemm_dense(const GemmArgs &g, const GemmWorkspace &ws, hipStream_t s)
 
 std::string gemm_kernel_name(const GemmArgs &g, int64_t ws_bytes, bool im2col) {
     if (im2col && patch_cc(g)) return g.KW == 3 ? "k_conv_patch<3, 2>" : "k_conv_patch<2, 1>";
+    if (im2col && frag_ok(g)) return "k_conv_frag<" + std::to_string(frag_waves(g)) + ">";
     const GemmPlan p = gemm_plan(g, ws_bytes, im2col);
     if (p.cfg == kCfgSmall)
         return std::string("k_gemm_small<") + (g.a_rowmajor ? "1, " : "0, ") +
