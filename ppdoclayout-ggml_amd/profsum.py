@@ -2,6 +2,9 @@
 
   python profsum.py stats   <kernel_stats.csv>                 > table (markdown)
   python profsum.py traffic <fetch_dir> <write_dir> <copy_MiB> > per-kernel HBM bytes (JSON)
+  python profsum.py dispatches <fetch_dir> <write_dir> <copy_MiB> <count>
+                                                          > the first <count> library dispatches in
+                                                            launch order with their HBM bytes (markdown)
 
 stats: one row per kernel symbol: calls, mean and total duration.
 
@@ -80,10 +83,30 @@ def traffic(fetch_dir, write_dir, copy_mib):
             "kernels": kernels}
 
 
+def dispatches(fetch_dir, write_dir, copy_mib, count):
+    """First `count` library dispatches (launch order) with scaled FETCH/WRITE MB."""
+    copy_bytes = copy_mib * (1 << 20)
+    cols = {}
+    for counter, directory in (("FETCH_SIZE", fetch_dir), ("WRITE_SIZE", write_dir)):
+        disp = per_dispatch(directory, counter)
+        foreign = [v for (k, v) in disp.values() if "ppdl::" not in k]
+        if not foreign:
+            raise SystemExit("no calibration copy found in " + directory)
+        fac = copy_bytes / (max(foreign) * 1024.0)
+        mine = sorted(((int(d), k, v) for d, (k, v) in disp.items() if "ppdl::" in k))[:count]
+        cols[counter] = [(short(k), v * 1024.0 * fac / 1e6) for (_, k, v) in mine]
+    out = ["| # | kernel | FETCH MB | WRITE MB |", "|---|---|---|---|"]
+    for i, ((k, f), (k2, w)) in enumerate(zip(cols["FETCH_SIZE"], cols["WRITE_SIZE"])):
+        out.append("| %d | `%s` | %.2f | %.2f |" % (i, k if k == k2 else k + " / " + k2, f, w))
+    return "\n".join(out)
+
+
 if __name__ == "__main__":
     if len(sys.argv) >= 3 and sys.argv[1] == "stats":
         print(stats(sys.argv[2]))
     elif len(sys.argv) >= 5 and sys.argv[1] == "traffic":
         print(json.dumps(traffic(sys.argv[2], sys.argv[3], int(sys.argv[4])), indent=1, sort_keys=True))
+    elif len(sys.argv) >= 6 and sys.argv[1] == "dispatches":
+        print(dispatches(sys.argv[2], sys.argv[3], int(sys.argv[4]), int(sys.argv[5])))
     else:
         sys.exit(__doc__)
