@@ -2,6 +2,7 @@
 
   python profsum.py stats   <kernel_stats.csv>                 > table (markdown)
   python profsum.py traffic <fetch_dir> <write_dir> <copy_MiB> > per-kernel HBM bytes (JSON)
+  python profsum.py mfma <pmc_dir>                         > per-kernel MFMA counters (markdown)
   python profsum.py dispatches <fetch_dir> <write_dir> <copy_MiB> <count>
                                                           > the first <count> library dispatches in
                                                             launch order with their HBM bytes (markdown)
@@ -40,17 +41,15 @@ def stats(path):
     return "\n".join(out)
 
 
-def per_dispatch(directory, counter):
-    """{dispatch_id: (kernel, value summed over instances)}"""
-    acc = {}
+def per_dispatch(directory, counter, reduce=sum):
+    """{dispatch_id: (kernel, value reduced over instances)}"""
+    vals = {}
     for f in glob.glob(os.path.join(directory, "**", "*counter_collection.csv"), recursive=True):
         for r in csv.DictReader(open(f)):
             if r["Counter_Name"] != counter:
                 continue
-            d = r["Dispatch_Id"]
-            k, v = acc.get(d, (r["Kernel_Name"], 0.0))
-            acc[d] = (k, v + float(r["Counter_Value"]))
-    return acc
+            vals.setdefault(r["Dispatch_Id"], (r["Kernel_Name"], []))[1].append(float(r["Counter_Value"]))
+    return {d: (k, reduce(v)) for d, (k, v) in vals.items()}
 
 
 def traffic(fetch_dir, write_dir, copy_mib):
@@ -83,6 +82,47 @@ def traffic(fetch_dir, write_dir, copy_mib):
             "kernels": kernels}
 
 
+def mfma(directory):
+    """Per kernel: FP32 MFMA FLOP per dispatch (SQ_INSTS_VALU_MFMA_MOPS_F32 x 512),
+    XF32 MFMA instructions (SQ_INSTS_VALU_MFMA_XF32), MFMA busy share of SIMD
+    cycles and, with the kernel trace of the same run, the counted FLOP over the
+    dispatch duration.  The busy share is SQ_VALU_MFMA_BUSY_CYCLES (summed over
+    SIMDs) / (SIMDs x active cycles), where GRBM_GUI_ACTIVE arrives summed over
+    the XCDs and is divided by their count (Num_Xcc of the agent info)."""
+    names = ("SQ_INSTS_VALU_MFMA_MOPS_F32", "SQ_INSTS_VALU_MFMA_XF32", "SQ_VALU_MFMA_BUSY_CYCLES", "GRBM_GUI_ACTIVE")
+    per = {n: per_dispatch(directory, n) for n in names}
+    dur = {}
+    for f in glob.glob(os.path.join(directory, "**", "*kernel_trace.csv"), recursive=True):
+        for r in csv.DictReader(open(f)):
+            dur[r["Dispatch_Id"]] = float(r["End_Timestamp"]) - float(r["Start_Timestamp"])
+    simds, xcc = 1024, 8
+    for f in glob.glob(os.path.join(directory, "**", "*agent_info.csv"), recursive=True):
+        for r in csv.DictReader(open(f)):
+            if r.get("Name", "").startswith("gfx"):
+                simds, xcc = int(r["Simd_Count"]), int(r["Num_Xcc"])
+    agg = defaultdict(lambda: [0, 0.0, 0.0, 0.0, 0.0, 0.0])  # n, flop, xf32, busy, active, ns
+    for d, (k, mops) in per[names[0]].items():
+        if "ppdl::" not in k:
+            continue
+        a = agg[short(k)]
+        a[0] += 1
+        a[1] += mops * 512.0
+        a[2] += per[names[1]].get(d, (k, 0.0))[1]
+        a[3] += per[names[2]].get(d, (k, 0.0))[1]
+        a[4] += per[names[3]].get(d, (k, 0.0))[1]
+        a[5] += dur.get(d, 0.0)
+    out = ["| kernel | dispatches | MFMA FP32 GFLOP per dispatch | XF32 MFMA instr | MFMA busy % | us per dispatch "
+           "(counter run) | counted TF/s |", "|---|---|---|---|---|---|---|"]
+    for k, (n, fl, xf, busy, act, ns) in sorted(agg.items(), key=lambda kv: -kv[1][1]):
+        if fl <= 0:
+            continue
+        util = 100.0 * busy / (act / xcc * simds) if act > 0 else 0.0
+        us = ns / n / 1e3 if ns > 0 else 0.0
+        tf = fl / ns / 1e3 if ns > 0 else 0.0
+        out.append("| `%s` | %d | %.4f | %d | %.1f | %.2f | %.1f |" % (k, n, fl / n / 1e9, xf, util, us, tf))
+    return "\n".join(out)
+
+
 def dispatches(fetch_dir, write_dir, copy_mib, count):
     """First `count` library dispatches (launch order) with scaled FETCH/WRITE MB."""
     copy_bytes = copy_mib * (1 << 20)
@@ -106,6 +146,8 @@ if __name__ == "__main__":
         print(stats(sys.argv[2]))
     elif len(sys.argv) >= 5 and sys.argv[1] == "traffic":
         print(json.dumps(traffic(sys.argv[2], sys.argv[3], int(sys.argv[4])), indent=1, sort_keys=True))
+    elif len(sys.argv) >= 3 and sys.argv[1] == "mfma":
+        print(mfma(sys.argv[2]))
     elif len(sys.argv) >= 6 and sys.argv[1] == "dispatches":
         print(dispatches(sys.argv[2], sys.argv[3], int(sys.argv[4]), int(sys.argv[5])))
     else:
