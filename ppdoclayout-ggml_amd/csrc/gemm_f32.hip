@@ -1106,7 +1106,10 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(const float *__restrict__
 // Operand order per chunk (kb = chunk start): step s = 4c + j (c < 4, j < 4)
 // pairs k = kb + 8c + j (lanes 0-31) with k = kb + 8c + 4 + j (lanes 32-63);
 // A and B use the same pairing, so the sum covers every k once.  A row-major
-// (AMODE 1) is then one float4 per lane per c.
+// (AMODE 1) is then one float4 per lane per c.  AMODE 2 computes A in the
+// loader: A[m][k] = relu(b4[k] + sum_j X[m][j] W4[j][k]) for a 4-column X
+// (its row is one float4 per lane, loaded once; W4 and b4 are read as float4
+// along k, the same address across a half-wave).
 constexpr int kSmallKC = 32;
 
 template <int AMODE, int WV, bool PRE>
@@ -1130,13 +1133,27 @@ __global__ __launch_bounds__(WV * 64) void k_gemm_small(GemmArgs g, int tiles_m,
     const bool pre = PRE && n0 < g.a_add_n;
     const int mc = min(m0 + l32, M - 1), nc = min(n0 + l32, N - 1);
     const int nchunk = (K + KC - 1) / KC;
+    const float4 xr = AMODE == 2 ? ld4(A + (uint32_t)(mc * lda)) : float4{0.0f, 0.0f, 0.0f, 0.0f};
 
     auto load = [&](float (&a)[NS], float (&b)[NS], int ch) {
         const int kb = ch * KC;
 #pragma unroll
         for (int c = 0; c < KC / 8; c++) {
             const int k4 = kb + 8 * c + 4 * h;  // this lane's 4 consecutive k
-            if (AMODE == 1) {
+            if (AMODE == 2) {
+                const int kk = min(k4, K - 4);
+                const float4 w0 = ld4(g.a_w4 + kk), w1 = ld4(g.a_w4 + K + kk);
+                const float4 w2 = ld4(g.a_w4 + 2 * K + kk), w3 = ld4(g.a_w4 + 3 * K + kk);
+                const float4 bb = ld4(g.a_b4 + kk);
+                const bool in = k4 < K;
+                const float v[4] = {
+                    fmaf(xr.w, w3.x, fmaf(xr.z, w2.x, fmaf(xr.y, w1.x, fmaf(xr.x, w0.x, bb.x)))),
+                    fmaf(xr.w, w3.y, fmaf(xr.z, w2.y, fmaf(xr.y, w1.y, fmaf(xr.x, w0.y, bb.y)))),
+                    fmaf(xr.w, w3.z, fmaf(xr.z, w2.z, fmaf(xr.y, w1.z, fmaf(xr.x, w0.z, bb.z)))),
+                    fmaf(xr.w, w3.w, fmaf(xr.z, w2.w, fmaf(xr.y, w1.w, fmaf(xr.x, w0.w, bb.w))))};
+#pragma unroll
+                for (int j = 0; j < 4; j++) a[4 * c + j] = in ? fmaxf(v[j], 0.0f) : 0.0f;
+            } else if (AMODE == 1) {
                 // K % 4 == 0: the 4 k are all inside or all outside
                 const uint32_t ai = (uint32_t)(mc * lda + min(k4, K - 4));
                 float4 v = ld4(A + ai);
@@ -1427,6 +1444,14 @@ hipError_t dispatch(const GemmArgs &g_in, const GemmWorkspace &ws, hipStream_t s
         if (const int cc = patch_cc(g)) return launch_patch(g, cc, s);
         if (frag_ok(g)) return launch_frag(g, s);
     }
+    if (g.a_w4) {
+        // A = relu(X W4 + b4): the small kernel's computed-A loader
+        const auto a16 = [](const void *q) { return (((uintptr_t)q) & 15) == 0; };
+        if (BMODE != 0 || !g.a_rowmajor || g.a_add || !g.a_b4 || g.lda != 4 || g.K % 4 != 0 || !a16(g.A) ||
+            !a16(g.a_w4) || !a16(g.a_b4))
+            return hipErrorInvalidValue;
+        return launch_small<2>(g, s);
+    }
     const GemmPlan p = gemm_plan(g, ws.bytes, BMODE == 1);
     if (g.a_add && (BMODE != 0 || !g.a_rowmajor || (((uintptr_t)g.a_add) & 15) != 0 || g.a_add_n % 32 != 0))
         return hipErrorInvalidValue;
@@ -1489,6 +1514,7 @@ GemmPlan gemm_plan(const GemmArgs &g, int64_t ws_bytes, bool im2col) {
 }
 
 int64_t gemm_ws_bytes_for(const GemmArgs &g, bool im2col) {
+    if (g.a_w4) return 0;  // the small kernel, no split-K
     if (im2col && !patch_cc(g) && frag_ok(g)) return 0;  // the fragment kernel splits K inside a block
     const GemmPlan p = gemm_plan(g, INT64_MAX, im2col);
     return gemm_ws_bytes(g.M, g.N, g.batch, p.cfg, p.splits);
@@ -1499,6 +1525,7 @@ hipError_t gemm_dense(const GemmArgs &g, const GemmWorkspace &ws, hipStream_t s)
 std::string gemm_kernel_name(const GemmArgs &g, int64_t ws_bytes, bool im2col) {
     if (im2col && patch_cc(g)) return g.KW == 3 ? "k_conv_patch<3, 2>" : "k_conv_patch<2, 1>";
     if (im2col && frag_ok(g)) return "k_conv_frag<" + std::to_string(frag_waves(g)) + ">";
+    if (g.a_w4) return "k_gemm_small<2, " + std::to_string(small_waves(g.K, small_tiles(g))) + ", false>";
     const GemmPlan p = gemm_plan(g, ws_bytes, im2col);
     if (p.cfg == kCfgSmall)
         return std::string("k_gemm_small<") + (g.a_rowmajor ? "1, " : "0, ") +

@@ -271,6 +271,7 @@ class Net {
             int add_mode = 0, const float *a_add = nullptr, int a_add_n = 0);
     Seq ln(const Seq &a, const float *b, const std::string &name, float *out = nullptr, int out_chw = 0);
     Seq mlp3(const Seq &x, const std::string &pfx);
+    Seq lin_in4(const Seq &x, const std::string &first, const std::string &second, int act);
     Seq mha(const Seq &x, const float *pos, const std::string &pfx, float *out, const float *resid);
     void hg_block(const Img &cat, int cin, const std::string &pfx, bool light, int mid, Img *y, float *out,
                   const float *resid);
@@ -513,6 +514,36 @@ Seq Net::ln(const Seq &a, const float *b, const std::string &name, float *out, i
     return y;
 }
 
+// second(relu(first(x))) for a 4-column x (the query-position MLP,
+// :824-826) as one GEMM: the 4-in ReLU layer is computed in the second
+// layer's A-operand loader, so its 300 x 512 hidden rows never reach memory
+Seq Net::lin_in4(const Seq &x, const std::string &first, const std::string &second, int act) {
+    const auto &n0 = shape(first + ".weight");   // (4, hidden)
+    const auto &n1 = shape(second + ".weight");  // (hidden, out)
+    if ((x.D != 4 || n0[0] != 4 || n1[0] != n0[1]) && bad_node_.empty()) bad_node_ = second + " (feature mismatch)";
+    const int hid = (int)n0[1], nout = (int)n1[1];
+    Seq y{alloc((int64_t)x.T * nout), x.T, nout, nout};
+    GemmArgs g{};
+    g.A = x.d;
+    g.lda = x.ld;
+    g.a_rowmajor = 1;
+    g.a_w4 = W(first + ".wt");
+    g.a_b4 = W(first + ".bias");
+    g.B = W(second + ".wt");
+    g.ldb = nout;
+    g.C = y.d;
+    g.ldc = nout;
+    g.bias = W(second + ".bias");
+    g.bias_n = 1;
+    g.M = x.T;
+    g.N = nout;
+    g.K = hid;
+    g.batch = 1;
+    g.act = act;
+    gemm(second, g);
+    return y;
+}
+
 Seq Net::mlp3(const Seq &x, const std::string &pfx) {
     Seq h = lin(x, pfx + ".0", kActRelu);
     h = lin(h, pfx + ".1", kActRelu);
@@ -751,7 +782,7 @@ bool Net::build(bool dumps, std::string *err) {
     Seq xq = target;
     for (int i = 0; i < 6; i++) {
         const std::string dp = "dec" + std::to_string(i);
-        Seq qpos = lin(lin(ref, "qpos.0", kActRelu), "qpos.1", kActNone);
+        Seq qpos = lin_in4(ref, "qpos.0", "qpos.1", kActNone);
         Seq sa = mha(xq, qpos.d, dp + ".sa", nullptr, xq.d);  // x + attn, q = k = x + qpos
         xq = ln(sa, nullptr, dp + ".ln1");
         if (i == 0) join(2);

@@ -78,6 +78,13 @@ struct GemmArgs {
     const float *add;
     const float *a_add;  // nullptr: none; a_add_n is then ignored
     int a_add_n;         // a multiple of 32
+    // A computed in the loader (small-GEMM kernel only): with a_w4 set, the A
+    // operand is relu(X W4 + b4) for the 4-column row-major X in A / lda,
+    // W4 = a_w4[4][K] (row j at a_w4 + j*K) and b4 = a_b4[K]; K % 4 == 0.
+    // It fuses a 4-in ReLU linear (the decoder's query-position MLP input)
+    // into the GEMM that consumes it.
+    const float *a_w4;
+    const float *a_b4;
 };
 
 // act codes of the GEMM epilogue and the elementwise kernels
