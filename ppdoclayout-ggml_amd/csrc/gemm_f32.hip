@@ -604,9 +604,19 @@ __device__ __forceinline__ uint64_t uniform_ptr(const float *p) {
 // per stage let the compiler move the accumulators between register files at
 // every tile.  A wave reads all of its fragments of a tile before the tile's
 // MFMAs, so the chain waits for LDS once per tile.
-template <int BM, int BN, int WGM, bool SPLIT, int NS, int KG>
-__global__ __launch_bounds__(kThreads * KG) void k_gemm_dma(GemmArgs g, SplitArgs sp, int tiles_m, int tiles_mn) {
+//
+// TAIL (64x64, KG = 2, no split): balances the last round of tiles.  Each XCD
+// holds a contiguous range of cnt tiles on its `cus` CUs; when the remainder
+// r = cnt mod cus is at most cus / 2, the last r tiles of the range run as 2r
+// half tiles (32 columns each), so the CUs that take a third (fourth, ...)
+// block take half a tile's work.  A half tile's work goes to waves 0-3 (one
+// per SIMD: two 32-row positions x the two k groups); waves 4-7 only share
+// the copies.  Blocks past an XCD's count exit at once.
+template <int BM, int BN, int WGM, bool SPLIT, int NS, int KG, bool TAIL = false>
+__global__ __launch_bounds__(kThreads * KG) void k_gemm_dma(GemmArgs g, SplitArgs sp, int tiles_m, int tiles_mn,
+                                                            int cus) {
     static_assert(NS >= 2 && NS <= 4 && (KG == 1 || KG == 2), "stages / groups");
+    static_assert(!TAIL || (BM == 64 && BN == 64 && WGM == 2 && KG == 2 && !SPLIT), "tail layout");
     constexpr int NT = kThreads * KG;
     constexpr int WGN = 4 / WGM, WM = BM / WGM, WN = BN / WGN, TM = WM / 32, TN = WN / 32;
     constexpr int IA = kBK * BM / 4 / NT, IB = kBK * BN / 4 / NT;  // copies per wave per tile
@@ -617,8 +627,30 @@ __global__ __launch_bounds__(kThreads * KG) void k_gemm_dma(GemmArgs g, SplitArg
     float *const As = smem, *const Bs = smem + NS * SA;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int grp = wave >> 2, wq = wave & 3;  // k group, position in the 2-d wave grid
-    const int logical = xcd_remap(blockIdx.x, gridDim.x);
+    int grp = wave >> 2, wq = wave & 3;  // k group, position in the 2-d wave grid
+    int logical, half = -1;              // half: which 32 columns of a half tile
+    if constexpr (TAIL) {
+        const int T = tiles_mn * g.batch;
+        const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
+        const int q = T >> 3, rr = T & 7;
+        const int cnt = q + (xcd < rr ? 1 : 0), start = xcd * q + min(xcd, rr);
+        const int r = cnt % cus;
+        const int h = (r > 0 && 2 * r <= cus) ? r : 0;
+        const int nfull = cnt - h;
+        if (slot >= cnt + h) return;  // the whole block, before any barrier
+        if (slot < nfull) {
+            logical = start + slot;
+        } else {
+            const int j = slot - nfull;
+            logical = start + nfull + (j >> 1);
+            half = j & 1;
+            grp = (wave >> 1) & 1;  // waves 0-3: 32-row position wave & 1, k group
+            wq = wave & 1;
+        }
+    } else {
+        logical = xcd_remap(blockIdx.x, gridDim.x);
+    }
+    const bool active = !TAIL || half < 0 || wave < 4;  // wave-uniform
     const int S = SPLIT ? sp.splits : 1;
     const int split = SPLIT ? logical % S : 0;
     const int tile_id = SPLIT ? logical / S : logical;
@@ -671,7 +703,7 @@ __global__ __launch_bounds__(kThreads * KG) void k_gemm_dma(GemmArgs g, SplitArg
         for (int j = 0; j < TN; j++)
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
-    const int wm0 = (wq % WGM) * WM, wn0 = (wq / WGM) * WN;
+    const int wm0 = (wq % WGM) * WM, wn0 = half >= 0 ? half * 32 : (wq / WGM) * WN;
     const int l32 = lane & 31;
     // this half-wave's k rows of a tile: kr .. kr + 2*KQ... (lanes 32-63 from row 16)
     const int kr = (lane >> 5) * KH + KQ * grp;
@@ -728,7 +760,7 @@ __global__ __launch_bounds__(kThreads * KG) void k_gemm_dma(GemmArgs g, SplitArg
             // deeper pipelines keep a fixed copy count per trip for their
             // vmcnt accounting and repeat the last tile instead.
             if (NS > 2 || i + 1 < nk) issue((i + NS - 1) % NS, min(kt + NS - 1, klast));
-            compute(u);
+            if (active) compute(u);
         }
         wait_vmcnt<0>();  // no copy may still target this block's LDS when it exits
     }
@@ -742,6 +774,10 @@ __global__ __launch_bounds__(kThreads * KG) void k_gemm_dma(GemmArgs g, SplitArg
         __syncthreads();  // every wave's last compute() has read its operands
         float *give = smem + (grp * 4 + wq) * HALF + lane;
         const float *take = smem + ((1 - grp) * 4 + wq) * HALF + lane;
+        if (!active) {
+            __syncthreads();  // the working waves' exchange
+            return;
+        }
         if (grp == 0) {
 #pragma unroll
             for (int i = 0; i < TM; i++)
@@ -1358,18 +1394,60 @@ int dma_groups() {
     return kg == 1 ? 1 : 2;
 }
 
+// CUs per XCD of the current device (blocks go to the 8 XCDs round-robin), 0
+// if unknown
+int cus_per_xcd() {
+    static int cached[16] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 16) return 0;
+    if (cached[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) n = 0;
+        cached[dev] = n >= 16 ? n / 8 : -1;
+    }
+    return cached[dev] > 0 ? cached[dev] : 0;
+}
+
+// Grid of the tail-balanced 64x64 launch for T tiles: 8 x the largest
+// per-XCD block count, or 0 when no XCD has a remainder of at most half its
+// CUs (PPDL_DMA_TAIL=0 turns the mode off).
+int64_t tail_grid(int64_t T) {
+    static const bool off = [] {
+        const char *e = getenv("PPDL_DMA_TAIL");
+        return e && e[0] == '0';
+    }();
+    const int cus = cus_per_xcd();
+    if (off || cus < 2 || T < 8 || T > 0x3fffffff) return 0;
+    int64_t most = 0;
+    bool any = false;
+    for (int x = 0; x < 8; x++) {
+        const int64_t cnt = T / 8 + (x < T % 8 ? 1 : 0);
+        const int64_t r = cnt % cus, h = (r > 0 && 2 * r <= cus) ? r : 0;
+        any = any || h > 0;
+        most = std::max(most, cnt + h);
+    }
+    return any ? 8 * most : 0;
+}
+
 template <int BM, int BN, int WGM, bool SPLIT>
 void launch_dma(const GemmArgs &g, const SplitArgs &sp, int64_t total, int tiles_m, int tiles_n, hipStream_t s) {
     // 8 waves need at least one 16-byte copy per operand and wave
     if constexpr (kBK * BM / 4 >= 2 * kThreads && kBK * BN / 4 >= 2 * kThreads) {
         if (dma_groups() == 2) {
+            if constexpr (BM == 64 && BN == 64 && WGM == 2 && !SPLIT) {
+                if (const int64_t grid = tail_grid(total)) {
+                    hipLaunchKernelGGL((k_gemm_dma<64, 64, 2, false, 2, 2, true>), dim3((unsigned)grid),
+                                       dim3(2 * kThreads), 0, s, g, sp, tiles_m, tiles_m * tiles_n, cus_per_xcd());
+                    return;
+                }
+            }
             hipLaunchKernelGGL((k_gemm_dma<BM, BN, WGM, SPLIT, 2, 2>), dim3((unsigned)total), dim3(2 * kThreads), 0,
-                               s, g, sp, tiles_m, tiles_m * tiles_n);
+                               s, g, sp, tiles_m, tiles_m * tiles_n, 0);
             return;
         }
     }
     hipLaunchKernelGGL((k_gemm_dma<BM, BN, WGM, SPLIT, 2, 1>), dim3((unsigned)total), dim3(kThreads), 0, s, g, sp,
-                       tiles_m, tiles_m * tiles_n);
+                       tiles_m, tiles_m * tiles_n, 0);
 }
 
 template <int BM, int BN, int WGM, int AMODE, int BMODE>
@@ -1535,8 +1613,10 @@ std::string gemm_kernel_name(const GemmArgs &g, int64_t ws_bytes, bool im2col) {
     char buf[96];
     if (!im2col && dma_ok(g)) {
         const int kg = (kBK * bm / 4 >= 2 * kThreads && kBK * bn / 4 >= 2 * kThreads) ? dma_groups() : 1;
-        snprintf(buf, sizeof(buf), "k_gemm_dma<%d, %d, %d, %s, 2, %d>%s", bm, bn, wgm, p.splits > 1 ? "true" : "false",
-                 kg, p.splits > 1 ? "+k_splitk_reduce" : "");
+        const bool tail = kg == 2 && bm == 64 && bn == 64 && wgm == 2 && p.splits == 1 &&
+                          tail_grid((int64_t)((g.M + 63) / 64) * ((g.N + 63) / 64) * g.batch) > 0;
+        snprintf(buf, sizeof(buf), "k_gemm_dma<%d, %d, %d, %s, 2, %d%s>%s", bm, bn, wgm, p.splits > 1 ? "true" : "false",
+                 kg, tail ? ", true" : "", p.splits > 1 ? "+k_splitk_reduce" : "");
     } else {
         const bool two_tap = im2col && ((g.IC >= kBK && !(g.IC % kBK == 0 && g.K % kBK == 0)) || g.IC == kBK / 2) &&
                              (p.cfg == 3 || p.cfg == 5);
