@@ -192,6 +192,12 @@ def run_network(args):
         g["bytes"] += n["bytes"]
         g["launches"] += 1
     dom_name, dom = max(groups.items(), key=lambda kv: kv[1]["us"])
+    # every single-kernel GEMM group, largest per-image time first
+    gemm_kernels = [{"kernel": k, "launches": v["launches"], "us_per_image": round(v["us"], 1),
+                     "us_per_launch": round(v["us"] / v["launches"], 2),
+                     "tflops": round(v["flops"] / (v["us"] * 1e-6) / 1e12, 2),
+                     "frac": round(v["flops"] / (v["us"] * 1e-6) / 1e12 / PEAK_FP32_MFMA_TFLOPS, 4)}
+                    for k, v in sorted(groups.items(), key=lambda kv: -kv[1]["us"])]
     dom_us = dom["us"] / dom["launches"]
     dom_fl = dom["flops"] / dom["launches"]
     dom_tf = dom_fl / (dom_us * 1e-6) / 1e12
@@ -252,6 +258,7 @@ def run_network(args):
             "node_us_sum": round(sum(n["us"] for n in nodes), 1),
         },
         "roofline": roofline,
+        "gemm_kernels": gemm_kernels,
         "cpu_baseline": cpu,
         "replay_ms": {"median": round(pct(0.5), 4), "p10": round(pct(0.1), 4), "p90": round(pct(0.9), 4),
                       "replays": len(per)},

@@ -1615,8 +1615,8 @@ std::string gemm_kernel_name(const GemmArgs &g, int64_t ws_bytes, bool im2col) {
         const int kg = (kBK * bm / 4 >= 2 * kThreads && kBK * bn / 4 >= 2 * kThreads) ? dma_groups() : 1;
         const bool tail = kg == 2 && bm == 64 && bn == 64 && wgm == 2 && p.splits == 1 &&
                           tail_grid((int64_t)((g.M + 63) / 64) * ((g.N + 63) / 64) * g.batch) > 0;
-        snprintf(buf, sizeof(buf), "k_gemm_dma<%d, %d, %d, %s, 2, %d%s>%s", bm, bn, wgm, p.splits > 1 ? "true" : "false",
-                 kg, tail ? ", true" : "", p.splits > 1 ? "+k_splitk_reduce" : "");
+        snprintf(buf, sizeof(buf), "k_gemm_dma<%d, %d, %d, %s, 2, %d, %s>%s", bm, bn, wgm,
+                 p.splits > 1 ? "true" : "false", kg, tail ? "true" : "false", p.splits > 1 ? "+k_splitk_reduce" : "");
     } else {
         const bool two_tap = im2col && ((g.IC >= kBK && !(g.IC % kBK == 0 && g.K % kBK == 0)) || g.IC == kBK / 2) &&
                              (p.cfg == 3 || p.cfg == 5);
