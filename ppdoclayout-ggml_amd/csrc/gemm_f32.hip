@@ -1410,12 +1410,11 @@ int cus_per_xcd() {
 
 // Grid of the tail-balanced 64x64 launch for T tiles: 8 x the largest
 // per-XCD block count, or 0 when no XCD has a remainder of at most half its
-// CUs (PPDL_DMA_TAIL=0 turns the mode off).
+// CUs (PPDL_DMA_TAIL=0 turns the mode off; read at every launch, so a test
+// can compare both modes in one process).
 int64_t tail_grid(int64_t T) {
-    static const bool off = [] {
-        const char *e = getenv("PPDL_DMA_TAIL");
-        return e && e[0] == '0';
-    }();
+    const char *e = getenv("PPDL_DMA_TAIL");
+    const bool off = e && e[0] == '0';
     const int cus = cus_per_xcd();
     if (off || cus < 2 || T < 8 || T > 0x3fffffff) return 0;
     int64_t most = 0;

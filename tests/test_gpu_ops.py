@@ -598,6 +598,42 @@ def test_topk(hip, orc, with_ws):
     assert np.array_equal(run(small, 50), orc.topk(small, 50))
 
 
+# ---------------------------------------------------------------- tail balancing
+@pytest.mark.parametrize("kind,IC,OC,H,W", [
+    ("conv1x1", 512, 256, 100, 100),  # config 1: 628 tiles, 14-15 tail tiles per XCD
+    ("conv1x1", 96, 200, 60, 167),    # 4 x 157 tiles, ragged M and N edges inside the tail
+    ("madd", 96, 192, 1, 640),        # 36 planes x 3 x 10 tiles: 7 tail tiles per XCD
+])
+def test_dma_tail_balancing_bit_identical(hip, orc, kind, IC, OC, H, W, monkeypatch):
+    """The balanced-tail launch of the 64x64 direct-to-LDS GEMM (each XCD's
+    last round as half tiles) against the plain launch (PPDL_DMA_TAIL=0): the
+    same k split and sum order, so bit-identical, and both at the oracle's
+    tolerance."""
+    say(f"tail balancing {kind} {IC}->{OC} @{H}x{W}")
+    rng = np.random.default_rng(IC + OC + W)
+    outs = []
+    if kind == "conv1x1":
+        x, w, b = conv_inputs(rng, IC, H, W, OC, 1)
+        for flag in ("1", "0"):
+            monkeypatch.setenv("PPDL_DMA_TAIL", flag)
+            outs.append(host(hip_conv1x1(hip, x, w, b, 1)[0]))
+        ref = orc.conv2d_ref(x, w, b, 1, 0, 1)
+    else:
+        T = W
+        dt = rng.random((36, IC, T)).astype(np.float32)
+        wg = (rng.standard_normal((36, IC, OC)) / np.sqrt(IC)).astype(np.float32)
+        for flag in ("1", "0"):
+            monkeypatch.setenv("PPDL_DMA_TAIL", flag)
+            yt = torch.full((36, OC, T), float("nan"), device="cuda")
+            hip.run_checked(hip.OP_WG4_MADD, yt, with_ws(hip, hip.OP_WG4_MADD, yt, [dev(dt), dev(wg)]))
+            outs.append(host(yt))
+        ref = np.einsum("pko,pkt->pot", wg.astype(np.float64), dt.astype(np.float64))
+    assert np.isfinite(outs[0]).all()
+    assert np.array_equal(outs[0], outs[1])
+    e = normwise(outs[0], ref)
+    say(f"  normwise {e:.2e}")
+    assert e < TOL
+
 # ---------------------------------------------------------------- graph capture
 def test_ops_replay_under_graph_capture(hip):
     """Every op is capture-safe: a captured sequence replays to the eager
