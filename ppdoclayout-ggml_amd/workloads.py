@@ -1,6 +1,7 @@
-"""The BASELINE workloads of the tagged-op path, as ready-to-launch op lists.
+"""The single-op benchmark workloads of the tagged-op path (1x1 conv, the F(4,3)
+sweep, the im2col convs, MSDeformAttn), as ready-to-launch op lists.
 
-`ConvSuite` holds configs 1-4 at their real shapes: device-resident seeded
+`ConvSuite` holds them at their real shapes: device-resident seeded
 inputs, weights repacked once by the library's own repack (as the reference
 repacks at load, src/ppdoclayout.cpp:251-346), intermediate buffers, and the
 tagged-op nodes that one pass enqueues.  Every launch goes through the C-ABI

@@ -7,7 +7,7 @@ oracle on the same inputs:
     FP32 budget), plus the float64 truth where the size allows;
   * Winograd input transform, im2col, top-k: bit-exact (same arithmetic or
     pure data movement); output transform bit-exact without SiLU.
-Sizes include every BASELINE config (1x1 512->256 @100^2, the Winograd sweep,
+Sizes include every benchmark configuration (1x1 512->256 @100^2, the Winograd sweep,
 the im2col convs, MSDeformAttn at 300 queries) plus ragged edge shapes.
 """
 import os
