@@ -77,7 +77,7 @@ class ConvSuite:
         self.host = {} if keep_host else None
         f32 = 4.0
 
-        # config 1: 1x1 512->256 @100x100, bias + ReLU fused (op 14)
+        # 1x1 512->256 @100x100, bias + ReLU fused (op 14)
         x = rng.random((512, 100, 100)).astype(np.float32)
         w, b = _conv_weights(rng, 512, 256, 1)
         wr, _ = H.repack_conv(w)
@@ -88,7 +88,7 @@ class ConvSuite:
         if keep_host:
             self.host["c1"] = (x, w, b, out)
 
-        # config 2: Winograd F(4,3) sweep, SiLU
+        # Winograd F(4,3) sweep, SiLU
         for (C, Hh, W) in WINOGRAD_SWEEP:
             x = rng.random((C, Hh, W)).astype(np.float32)
             w, b = _conv_weights(rng, C, C, 3)
@@ -109,7 +109,7 @@ class ConvSuite:
             if keep_host:
                 self.host[tag] = (x, w, b, out)
 
-        # config 3: implicit-im2col GEMM convs (op 16), act none
+        # implicit-im2col GEMM convs (op 16), act none
         for (IC, IH, IW, OC, K, S, Pd) in IM2COL_CONVS:
             x = rng.random((IC, IH, IW)).astype(np.float32)
             w, b = _conv_weights(rng, IC, OC, K)
@@ -124,7 +124,7 @@ class ConvSuite:
             if keep_host:
                 self.host[tag] = (x, w, b, out)
 
-        # config 4: MSDeformAttn sampling
+        # MSDeformAttn sampling, 300 queries
         val, off, awr, ref = msdef_inputs(rng)
         out = torch.empty((300, 256), device="cuda")
         self.nodes.append(Node("c4_msdeform", H.OP_MSDEF, out, [_dev(val), _dev(off), _dev(awr), _dev(ref)],

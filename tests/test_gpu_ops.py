@@ -141,8 +141,8 @@ def hip_conv_im2col(hip, x, w, b, K, S, P, act, use_ws=True):
 
 
 # ---------------------------------------------------------------- 1x1 conv
-def test_conv1x1_config1(hip, orc):
-    say("1x1 512->256 @100x100 relu (config 1)")
+def test_conv1x1_512_256_100(hip, orc):
+    say("1x1 512->256 @100x100 relu")
     rng = np.random.default_rng(SEED + 1)
     x, w, b = conv_inputs(rng, 512, 100, 100, 256, 1)
     out, (xt, wt, bt) = hip_conv1x1(hip, x, w, b, 1)
@@ -245,8 +245,8 @@ WG_CONFIGS = [(256, 100, 100), (256, 50, 50), (256, 25, 25), (48, 200, 200), (96
 
 
 @pytest.mark.parametrize("C,H,W", WG_CONFIGS)
-def test_winograd_config2(hip, orc, C, H, W):
-    say(f"winograd {C}->{C} @{H}x{W} silu (config 2)")
+def test_winograd_sweep(hip, orc, C, H, W):
+    say(f"winograd {C}->{C} @{H}x{W} silu")
     rng = np.random.default_rng(SEED + 2 + C + H)
     x, w, b = conv_inputs(rng, C, H, W, C, 3)
     out, dt, yt, wg4 = hip_winograd(hip, x, w, b, 2)
@@ -299,8 +299,8 @@ IM2COL_CONFIGS = [  # IC, IH, IW, OC, K, S, P
 
 @pytest.mark.parametrize("IC,IH,IW,OC,K,S,P", IM2COL_CONFIGS)
 @pytest.mark.parametrize("act", [0, 1, 2])
-def test_conv_im2col_config3(hip, orc, IC, IH, IW, OC, K, S, P, act):
-    say(f"im2col conv k{K}s{S}p{P} {IC}->{OC} @{IH}x{IW} act{act} (config 3)")
+def test_conv_im2col_bench_shapes(hip, orc, IC, IH, IW, OC, K, S, P, act):
+    say(f"im2col conv k{K}s{S}p{P} {IC}->{OC} @{IH}x{IW} act{act}")
     rng = np.random.default_rng(SEED + 3 + IC + IH + act)
     x, w, b = conv_inputs(rng, IC, IH, IW, OC, K)
     y = host(hip_conv_im2col(hip, x, w, b, K, S, P, act))
@@ -467,7 +467,7 @@ def test_bias_act(hip, orc, shape):
 
 
 # ---------------------------------------------------------------- MSDeformAttn
-def msdef_config4(rng, nq=300):
+def msdef_300q(rng, nq=300):
     """Config 4: values N(0,1); ref cx,cy U(0,1), w,h U(0.05,1); a normalised
     displacement d ~ N(0, 0.05) per sample, off = d*8/wh so loc = ref + d,
     then loc clamped to [-0.1, 1.1] (partly and fully out-of-bounds samples);
@@ -503,7 +503,7 @@ def test_msdeform_row_strided_value(hip, orc):
     wider projections (the runtime's six decoder layers share one 13125 x
     1536 value projection; offsets | logits come from one 288-wide GEMM):
     same result, bit for bit, as the contiguous inputs."""
-    val, off, awr, ref = msdef_config4(np.random.default_rng(SEED + 44))
+    val, off, awr, ref = msdef_300q(np.random.default_rng(SEED + 44))
     wide = torch.full((val.shape[0], 1536), float("nan"), device="cuda")
     wide[:, 512:768] = dev(val)
     v = col_slice_view(hip, wide, 512, 256)
@@ -526,9 +526,9 @@ def test_msdeform_row_strided_value(hip, orc):
     assert hip.run(hip.OP_MSDEF, out, [bad, dev(off), dev(awr), dev(ref)]) == hip.EINVAL  # rows overlap
 
 
-def test_msdeform_config4(hip, orc):
-    say("msdeform 300q x 8h x 3lvl x 4pt (config 4)")
-    val, off, awr, ref = msdef_config4(np.random.default_rng(SEED + 4))
+def test_msdeform_300q(hip, orc):
+    say("msdeform 300q x 8h x 3lvl x 4pt")
+    val, off, awr, ref = msdef_300q(np.random.default_rng(SEED + 4))
     y = hip_msdeform(hip, val, off, awr, ref)
     oref = orc.msdeform(val, off, awr, ref)
     e = normwise(y, oref)
@@ -551,7 +551,7 @@ def test_msdeform_fixture_and_special_cases(hip, orc):
     # odd query counts
     rng = np.random.default_rng(3)
     for nq in (1, 17):
-        v2, o2, a2, r2 = msdef_config4(rng, nq)
+        v2, o2, a2, r2 = msdef_300q(rng, nq)
         assert normwise(hip_msdeform(hip, v2, o2, a2, r2), orc.msdeform(v2, o2, a2, r2)) < TOL
 
 
@@ -600,7 +600,7 @@ def test_topk(hip, orc, with_ws):
 
 # ---------------------------------------------------------------- tail balancing
 @pytest.mark.parametrize("kind,IC,OC,H,W", [
-    ("conv1x1", 512, 256, 100, 100),  # config 1: 628 tiles, 14-15 tail tiles per XCD
+    ("conv1x1", 512, 256, 100, 100),  # 1x1 512->256 @100^2: 628 tiles, 14-15 tail tiles per XCD
     ("conv1x1", 96, 200, 60, 167),    # 4 x 157 tiles, ragged M and N edges inside the tail
     ("madd", 96, 192, 1, 640),        # 36 planes x 3 x 10 tiles: 7 tail tiles per XCD
 ])
@@ -651,7 +651,7 @@ def test_ops_replay_under_graph_capture(hip):
     yt = torch.empty((36, 64, T), device="cuda")
     mid = torch.empty((64, 50, 50), device="cuda")
     out = torch.empty((32, 50, 50), device="cuda")
-    val, off, awr, ref = msdef_config4(rng, 300)
+    val, off, awr, ref = msdef_300q(rng, 300)
     vt, ot, at, rt = dev(val), dev(off), dev(awr), dev(ref)
     ms = torch.empty((300, 256), device="cuda")
 
