@@ -129,6 +129,23 @@ PPDL_HIP_API int ppdl_hip_supports(const int32_t op_params[16], const ppdl_tview
 PPDL_HIP_API int ppdl_hip_run(const int32_t op_params[16], const ppdl_tview *dst,
                               const ppdl_tview *src, int nsrc, void *stream);
 
+/* Size of the device scratch array behind ppdl_hip_run_noalloc (16 MiB per
+ * GPU, held from the first call on that GPU until the process ends). */
+#define PPDL_HIP_NOALLOC_SCRATCH_BYTES (16LL << 20)
+
+/* ppdl_hip_run without a workspace argument and without any allocation.  No
+ * counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under hipGraph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  src holds the op's own sources only; the workspace
+ * ppdl_hip_run would take as an extra src comes from a file-scope device
+ * array of PPDL_HIP_NOALLOC_SCRATCH_BYTES, so results equal ppdl_hip_run's
+ * with a full workspace.  Nodes whose workspace (ppdl_hip_workspace_bytes)
+ * exceeds the array are rejected with PPDL_EINVAL and a message on stderr.
+ * Every call on one GPU shares that GPU's array: calls that overlap on one
+ * GPU (other streams, concurrent graph replays) race on it. */
+PPDL_HIP_API int ppdl_hip_run_noalloc(const int32_t op_params[16], const ppdl_tview *dst,
+                                      const ppdl_tview *src, int nsrc, void *stream);
+
 /* Workspace bytes the node would use (GEMM ops: its split-K plan, 0 = needs
  * none; op 13: 8 per token), or -1 if the node is invalid.  Host-only; no counterpart in the reference, whose
  * GEMMs run in cuBLAS with the backend's own workspace. */

@@ -109,6 +109,15 @@ hipError_t gemm_dense(const GemmArgs &g, const GemmWorkspace &ws, hipStream_t s)
 std::string gemm_kernel_name(const GemmArgs &g, int64_t ws_bytes, bool im2col);
 // GEMM description of a validated conv / madd tagged node (ppdl_ops.cpp)
 bool gemm_args_of(const int32_t *p, const ppdl_tview *dst, const ppdl_tview *src, GemmArgs *g, bool *im2col);
+// Tagged-node validation (magic, pointers, the op's contract): PPDL_OK,
+// PPDL_EINVAL or PPDL_UNSUPPORTED, touching no device (ppdl_ops.cpp)
+int check_node(const int32_t *p, const ppdl_tview *dst, const ppdl_tview *src, int nsrc);
+// Enqueue a node that check_node accepted.  ws, when not null, is the
+// workspace the node's kernels use instead of an attached workspace src.
+int run_node(const int32_t *p, const ppdl_tview *dst, const ppdl_tview *src, int nsrc, const GemmWorkspace *ws,
+             hipStream_t s);
+// src index of the op's optional workspace, or -1 for ops that take none
+int workspace_src_index(const int32_t *p);
 hipError_t gemm_im2col(const GemmArgs &g, const GemmWorkspace &ws, hipStream_t s);
 
 // ---- Winograd transforms ----

@@ -329,21 +329,12 @@ extern "C" PPDL_HIP_API int ppdl_hip_supports(const int32_t op_params[16], const
     return check_op(op_params, dst, src, nsrc) == PPDL_OK ? 1 : 0;
 }
 
-extern "C" PPDL_HIP_API int ppdl_hip_run(const int32_t op_params[16], const ppdl_tview *dst,
-                                         const ppdl_tview *src, int nsrc, void *stream) {
-    if (!op_params || (uint32_t)op_params[12] != (uint32_t)PPDL_MAGIC) return PPDL_UNSUPPORTED;
-    if (!dst || (nsrc > 0 && !src) || nsrc < 0) return PPDL_EINVAL;
-    const int rc = check_op(op_params, dst, src, nsrc);
-    if (rc != PPDL_OK) return rc;
-    const int32_t *p = op_params;
-    hipStream_t s = (hipStream_t)stream;
-
+int ppdl::run_node(const int32_t *p, const ppdl_tview *dst, const ppdl_tview *src, int nsrc,
+                   const GemmWorkspace *ws_in, hipStream_t s) {
     GemmArgs g;
     bool im2col;
-    if (args_of_node(p, dst, src, &g, &im2col)) {
-        const GemmWorkspace ws = ws_of(p, src, nsrc);
-        return status_of(im2col ? gemm_im2col(g, ws, s) : gemm_dense(g, ws, s));
-    }
+    const GemmWorkspace ws = ws_in ? *ws_in : ws_of(p, src, nsrc);
+    if (args_of_node(p, dst, src, &g, &im2col)) return status_of(im2col ? gemm_im2col(g, ws, s) : gemm_dense(g, ws, s));
 
     switch (p[13]) {
         case PPDL_OP_BIASACT: {
@@ -371,14 +362,27 @@ extern "C" PPDL_HIP_API int ppdl_hip_run(const int32_t op_params[16], const ppdl
                                       (const float *)src[3].data, (float *)dst->data, (int)dst->ne[1], s));
         case PPDL_OP_MASKBOX:
             return status_of(mask_box((const float *)src[0].data, (float *)dst->data, (int)dst->ne[1], s));
-        case PPDL_OP_TOPK: {
-            const GemmWorkspace ws = ws_of(p, src, nsrc);
+        case PPDL_OP_TOPK:
             return status_of(topk((const float *)src[0].data, (int32_t *)dst->data, (int)src[0].ne[1],
                                   (int)src[0].ne[0], (int)dst->ne[0], ws.base, ws.bytes, s));
-        }
         default:
             return PPDL_UNSUPPORTED;
     }
+}
+
+int ppdl::check_node(const int32_t *p, const ppdl_tview *dst, const ppdl_tview *src, int nsrc) {
+    if (!p || (uint32_t)p[12] != (uint32_t)PPDL_MAGIC) return PPDL_UNSUPPORTED;
+    if (!dst || (nsrc > 0 && !src) || nsrc < 0) return PPDL_EINVAL;
+    return check_op(p, dst, src, nsrc);
+}
+
+int ppdl::workspace_src_index(const int32_t *p) { return ws_index(p); }
+
+extern "C" PPDL_HIP_API int ppdl_hip_run(const int32_t op_params[16], const ppdl_tview *dst,
+                                         const ppdl_tview *src, int nsrc, void *stream) {
+    const int rc = check_node(op_params, dst, src, nsrc);
+    if (rc != PPDL_OK) return rc;
+    return run_node(op_params, dst, src, nsrc, nullptr, (hipStream_t)stream);
 }
 
 extern "C" PPDL_HIP_API int ppdl_hip_im2col_f32(const float *x, float *dst, int64_t IW, int64_t IH,

@@ -42,7 +42,10 @@ EXPORTS = (
     "ppdl_hip_repack_conv",
     "ppdl_hip_wg4_matrices",
     "ppdl_hip_workspace_bytes",
+    "ppdl_hip_run_noalloc",
 )
+
+NOALLOC_SCRATCH_BYTES = 16 << 20  # PPDL_HIP_NOALLOC_SCRATCH_BYTES
 
 
 class TView(ctypes.Structure):
@@ -80,6 +83,8 @@ def lib():
         L.ppdl_hip_supports.restype = ctypes.c_int
         L.ppdl_hip_run.argtypes = [i32p, tvp, tvp, ctypes.c_int, ctypes.c_void_p]
         L.ppdl_hip_run.restype = ctypes.c_int
+        L.ppdl_hip_run_noalloc.argtypes = [i32p, tvp, tvp, ctypes.c_int, ctypes.c_void_p]
+        L.ppdl_hip_run_noalloc.restype = ctypes.c_int
         L.ppdl_hip_im2col_f32.argtypes = [ctypes.c_void_p, ctypes.c_void_p] + [ctypes.c_int64] * 10 + [
             ctypes.c_int
         ] * 6 + [ctypes.c_void_p]
@@ -164,6 +169,14 @@ def run(op, dst, srcs, p14=0, p15=0, stream=None):
     d, arr, n = _views(dst, srcs)
     s = current_stream() if stream is None else stream
     return lib().ppdl_hip_run(params(op, p14, p15), ctypes.byref(d), arr, n, ctypes.c_void_p(s))
+
+
+def run_noalloc(op, dst, srcs, p14=0, p15=0, stream=None):
+    """Enqueue one tagged op through ppdl_hip_run_noalloc (the op's own srcs
+    only; its workspace comes from the library's device scratch array)."""
+    d, arr, n = _views(dst, srcs)
+    s = current_stream() if stream is None else stream
+    return lib().ppdl_hip_run_noalloc(params(op, p14, p15), ctypes.byref(d), arr, n, ctypes.c_void_p(s))
 
 
 def run_checked(op, dst, srcs, p14=0, p15=0, stream=None):

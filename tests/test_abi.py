@@ -159,6 +159,26 @@ def test_workspace_query_is_host_only(hip, monkeypatch):
     assert hip.workspace_bytes(hip.OP_CONV1X1_BA, v([4, 4, 9]), [v([4, 4, 8]), v([8, 8, 1]), v([8])], 0) == -1
 
 
+def test_noalloc_rejects_on_the_host(hip, monkeypatch):
+    """ppdl_hip_run_noalloc validates like ppdl_hip_run, refuses an attached
+    workspace src and a plan larger than its scratch array, all before any
+    device call (FAKE pointers are never dereferenced)."""
+    v = lambda ne: hip.raw_view(FAKE, ne)  # noqa: E731
+    L = hip.lib()
+
+    def call(op, dst, srcs, p14=0, p15=0):
+        d, arr, n = hip._views(dst, srcs)
+        return L.ppdl_hip_run_noalloc(hip.params(op, p14, p15), ctypes.byref(d), arr, n, None)
+
+    srcs = [v([25, 25, 4096]), v([1024, 4096, 1]), v([1024])]
+    assert call(hip.OP_CONV1X1_BA, v([25, 25, 1023]), srcs) == hip.EINVAL  # shape mismatch
+    assert call(42, v([4]), [v([4])]) == hip.UNSUPPORTED
+    assert call(hip.OP_CONV1X1_BA, v([25, 25, 1024]), srcs + [v([1 << 20])]) == hip.EINVAL  # workspace src
+    monkeypatch.setenv("PPDL_GEMM_TILE", "3,16")  # 16 x 1024 x 625 fp32 partials: 41 MB
+    assert hip.workspace_bytes(hip.OP_CONV1X1_BA, v([25, 25, 1024]), srcs) > hip.NOALLOC_SCRATCH_BYTES
+    assert call(hip.OP_CONV1X1_BA, v([25, 25, 1024]), srcs) == hip.EINVAL
+
+
 def test_misaligned_workspace_rejected(hip):
     v = lambda ne, p=FAKE: hip.raw_view(p, ne)  # noqa: E731
     srcs = [v([25, 25, 64]), v([32, 64, 1]), v([32]), v([1024], FAKE + 4)]
