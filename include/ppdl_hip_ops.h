@@ -152,6 +152,15 @@ PPDL_HIP_API int ppdl_hip_run_noalloc(const int32_t op_params[16], const ppdl_tv
 PPDL_HIP_API int64_t ppdl_hip_workspace_bytes(const int32_t op_params[16], const ppdl_tview *dst,
                                               const ppdl_tview *src, int nsrc);
 
+/* Name of the device kernel(s) ppdl_hip_run would launch for this node (with
+ * the workspace src it carries, if any), e.g. "k_gemm_dma<64, 64, 2, false,
+ * 2, 2, true>"; empty for ops that are not GEMMs.  Writes at most cap bytes
+ * including the terminator and returns the full length, or -1 if the node is
+ * invalid.  Launches nothing (it may read the current device's CU count).  No
+ * counterpart in the reference: a diagnostic for tests and profiles. */
+PPDL_HIP_API int ppdl_hip_kernel_name(const int32_t op_params[16], const ppdl_tview *dst,
+                                      const ppdl_tview *src, int nsrc, char *buf, int cap);
+
 /* F32 im2col in ggml's layout: dst[pix][k], pix = (n*OH + oh)*OW + ow,
  * k = ic*KH*KW + kh*KW + kw, zero where the tap falls outside the input.
  * Replaces ggml_cuda_ppdl_im2col_f32 (patches/ggml-ppdl.patch:885-906) with the

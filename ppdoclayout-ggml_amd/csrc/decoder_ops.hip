@@ -56,11 +56,14 @@ __global__ __launch_bounds__(256) void k_msdeform(const float *__restrict__ val,
     const float *vh = val + h * kHD + c;
     // Corner tokens and weights first, the 48 gathers next (all issued
     // together), the accumulation last in the reference's l -> p -> corner
-    // order.  A corner outside the map or with zero bilinear weight reads
-    // token 0 with weight 0: fmaf(0, v, acc) == acc, as if it were skipped.
+    // order.  A corner outside the map or with zero bilinear weight is
+    // skipped, as the reference skips it: its gather reads token 0 (any valid
+    // address) and a select, not a multiply by zero, leaves the sum as it was,
+    // so a non-finite value there cannot reach the output.
     constexpr int kS = 3 * 4 * 4;
     float wv[kS];
     int tok[kS];
+    bool use[kS];
 #pragma unroll
     for (int l = 0; l < 3; l++) {
         const int W = kLvlW[l], H = kLvlW[l], st = kLvlStart[l];
@@ -84,7 +87,8 @@ __global__ __launch_bounds__(256) void k_msdeform(const float *__restrict__ val,
                 const int xx = x0 + (k & 1), yy = y0 + (k >> 1);
                 const bool in = xx >= 0 && xx < W && yy >= 0 && yy < H && cw[k] != 0.0f;
                 const int i = (l * 4 + p) * 4 + k;
-                wv[i] = in ? wt * cw[k] : 0.0f;
+                use[i] = in;
+                wv[i] = wt * cw[k];
                 tok[i] = in ? st + yy * W + xx : 0;
             }
         }
@@ -94,7 +98,7 @@ __global__ __launch_bounds__(256) void k_msdeform(const float *__restrict__ val,
     for (int i = 0; i < kS; i++) v[i] = vh[(int64_t)tok[i] * ldv];
     float acc = 0.0f;
 #pragma unroll
-    for (int i = 0; i < kS; i++) acc = fmaf(wv[i], v[i], acc);
+    for (int i = 0; i < kS; i++) acc = use[i] ? fmaf(wv[i], v[i], acc) : acc;
     out[(int64_t)q * kDM + h * kHD + c] = acc;
 }
 

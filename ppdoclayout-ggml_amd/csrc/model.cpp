@@ -25,6 +25,7 @@
 #include <memory>
 #include <numeric>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "../../include/ppdl_hip_ops.h"
@@ -136,6 +137,9 @@ class Net {
     double time_graph(int iters);
     int profile_nodes(int iters, ppdl_node_stat *out, int cap);
     bool upload_image(const float *host);
+    // the host result's inputs: mask sign bits packed on the device, then
+    // logits, boxes, order and the bits copied into pinned buffers
+    bool download(float *logits, float *boxes, float *order, uint32_t *mbits);
 
     int nodes() const {
         int k = 0;
@@ -146,6 +150,7 @@ class Net {
     // outputs
     float *logits_ = nullptr, *boxes_ = nullptr, *order_ = nullptr, *masks_ = nullptr, *refu_ = nullptr;
     int32_t *topk_ = nullptr;
+    uint32_t *mbits_ = nullptr;  // sign bits of masks_, packed after a replay for the host result
     std::vector<DumpRec> dumps_;
 
    private:
@@ -252,7 +257,8 @@ class Net {
         bool im2col;
         if (gemm_args_of(pv.data(), &dst, src.data(), &g, &im2col)) gemm_meta(1, g, wsb, im2col);
     }
-    void gemm(const std::string &name, GemmArgs g) {
+    // cls: 2 linear (token-major) GEMM, 1 a conv that writes token-major
+    void gemm(const std::string &name, GemmArgs g, int cls = 2) {
         const int64_t wsb = gemm_ws_bytes_for(g, false);
         Scratch *sc = &sc_[lane_];
         sc->ws_need = std::max(sc->ws_need, wsb);
@@ -260,7 +266,7 @@ class Net {
             GemmWorkspace ws{wsb > 0 ? sc->ws : nullptr, wsb > 0 ? sc->ws_bytes : 0};
             return gemm_dense(g, ws, s) == hipSuccess ? 0 : 3;
         });
-        gemm_meta(2, g, wsb, false);
+        gemm_meta(cls, g, wsb, false);
     }
     static int ok(hipError_t e) { return e == hipSuccess ? 0 : 3; }
 
@@ -726,7 +732,7 @@ bool Net::build(bool dumps, std::string *err) {
             g.N = P;
             g.K = lv[l].C;
             g.batch = 1;
-            gemm(nm, g);
+            gemm(nm, g, 1);  // a 1x1 conv (src/ppdoclayout.cpp:786-788) stored token-major
         }
     }
     dump("source", source.d, {kDM, NTOK});
@@ -811,6 +817,7 @@ bool Net::build(bool dumps, std::string *err) {
     Seq mq6 = mlp3(outq, "mq");
     masks_ = alloc((int64_t)NQ * NPIX);
     masks_of(mq6, masks_, "masks");
+    mbits_ = (uint32_t *)alloc((int64_t)NQ * (NPIX / 32));
     Seq gp = lin(lin(xq, "order5", kActNone), "gp", kActNone);  // (300, 128)
     order_ = alloc((int64_t)NQ * NQ);
     node("order", 1, [=](hipStream_t st) { return ok(order_logits(gp.d, order_, NQ, 64, 1.0f / 8.0f, st)); });
@@ -936,6 +943,16 @@ bool Net::upload_image(const float *host) {
            hipStreamSynchronize(stream_) == hipSuccess;
 }
 
+bool Net::download(float *logits, float *boxes, float *order, uint32_t *mbits) {
+    const hipStream_t s = stream_;
+    return mask_bits(masks_, mbits_, NQ, NPIX, s) == hipSuccess &&
+           hipMemcpyAsync(logits, logits_, (size_t)NQ * NC * 4, hipMemcpyDeviceToHost, s) == hipSuccess &&
+           hipMemcpyAsync(boxes, boxes_, (size_t)NQ * 4 * 4, hipMemcpyDeviceToHost, s) == hipSuccess &&
+           hipMemcpyAsync(order, order_, (size_t)NQ * NQ * 4, hipMemcpyDeviceToHost, s) == hipSuccess &&
+           hipMemcpyAsync(mbits, mbits_, (size_t)NQ * (NPIX / 32) * 4, hipMemcpyDeviceToHost, s) == hipSuccess &&
+           hipStreamSynchronize(s) == hipSuccess;
+}
+
 int Net::replay() {
     if (hipGraphLaunch(exec_, stream_) != hipSuccess) return 2;
     return hipStreamSynchronize(stream_) == hipSuccess ? 0 : 2;
@@ -1006,57 +1023,114 @@ int Net::profile_nodes(int iters, ppdl_node_stat *out, int cap) {
 }
 
 // ---------------------------------------------------------------------------
-// Postprocess (src/ppdoclayout.cpp:927-993), on the host: reading-order votes,
-// top-300 over the 7500 class scores, box restore to the original size, mask
-// binarisation.
-void postprocess(const std::vector<float> &logits, const std::vector<float> &boxes, const std::vector<float> &order,
-                 const std::vector<float> &maskl, int ori_h, int ori_w, std::vector<float> &out0,
-                 std::vector<int32_t> &out2, std::vector<int32_t> &sel) {
-    std::vector<float> votes(NQ, 0.0f);
-    for (int j = 0; j < NQ; j++) {
-        float acc = 0.0f;
-        for (int i = 0; i < NQ; i++) {
-            if (i == j) continue;
-            const float diff = order[(size_t)j + (size_t)NQ * i] - order[(size_t)i + (size_t)NQ * j];
-            acc += 1.0f / (1.0f + std::exp(-diff));
-        }
-        votes[j] = acc;
-    }
-    std::vector<int> rank_of(NQ);
-    std::iota(rank_of.begin(), rank_of.end(), 0);
-    std::stable_sort(rank_of.begin(), rank_of.end(), [&](int a2, int b2) { return votes[a2] < votes[b2]; });
-    std::vector<int> order_seq(NQ);
-    for (int r = 0; r < NQ; r++) order_seq[rank_of[r]] = r;
+// Host result assembly: the reference's postprocess (src/ppdoclayout.cpp:
+// 927-993) on this runtime's downloads.  The device has packed the mask
+// logits into sign bits (mask_bits), so 1.5 MB crosses PCIe instead of 48 MB.
+// On the host:
+//   * every (query, class) logit is scored with the logistic function, and
+//     the 300 best are picked by a 64-bit key: the score's order-preserving
+//     bits, then the complemented flat index (lower index first on ties);
+//   * queries are placed in reading order by their pairwise-vote totals,
+//     keyed by (vote, query index) ascending;
+//   * the picked rows get label, score, the box restored to the original
+//     size, the reading position, and their query's mask bits expanded.
+// The float arithmetic (logistic as 1 / (1 + exp(-x)), each vote summed over
+// i ascending, the box formulas) is the reference's, so results match it bit
+// for bit.
+struct HostOut {
+    float *logits = nullptr, *boxes = nullptr, *order = nullptr;  // pinned downloads
+    uint32_t *mbits = nullptr;
+};
 
-    std::vector<float> scores((size_t)NQ * NC);
-    for (size_t i = 0; i < scores.size(); i++) scores[i] = 1.0f / (1.0f + std::exp(-logits[i]));
-    std::vector<int> flat(scores.size());
-    std::iota(flat.begin(), flat.end(), 0);
-    std::partial_sort(flat.begin(), flat.begin() + NQ, flat.end(), [&](int a2, int b2) {
-        if (scores[a2] != scores[b2]) return scores[a2] > scores[b2];
-        return a2 < b2;
-    });
-    const float sf_h = (float)IMG / (float)ori_h, sf_w = (float)IMG / (float)ori_w;
-    const float oh = std::floor((float)IMG / sf_h + 0.5f), ow = std::floor((float)IMG / sf_w + 0.5f);
-    out0.assign((size_t)NQ * 7, 0.0f);
-    out2.assign((size_t)NQ * NPIX, 0);
-    sel.assign(NQ, 0);
-    for (int r = 0; r < NQ; r++) {
-        const int f = flat[r], q = f / NC, c = f % NC;
-        sel[r] = f;
-        const float *b = boxes.data() + (size_t)q * 4;
-        float *o = out0.data() + (size_t)r * 7;
-        o[0] = (float)c;
-        o[1] = scores[f];
-        o[2] = (b[0] - b[2] * 0.5f) * ow;
-        o[3] = (b[1] - b[3] * 0.5f) * oh;
-        o[4] = (b[0] + b[2] * 0.5f) * ow;
-        o[5] = (b[1] + b[3] * 0.5f) * oh;
-        o[6] = (float)order_seq[q];
-        const float *m = maskl.data() + (size_t)q * NPIX;
-        int32_t *mo = out2.data() + (size_t)r * NPIX;
-        for (int p = 0; p < NPIX; p++) mo[p] = m[p] > 0.0f ? 1 : 0;
+inline float logistic(float x) { return 1.0f / (1.0f + std::exp(-x)); }
+
+// uint32 whose unsigned order is the float order, with -0 taken as +0 (the
+// two compare equal)
+inline uint32_t sortable_bits(float f) {
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    if (u == 0x80000000u) u = 0;
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// pos[j] = reading position of query j.  R[i][j] = order[i * nq + j]; the
+// vote of j sums logistic(R[i][j] - R[j][i]) over i != j in ascending i.
+// Row i of R is streamed once and adds its term to every vote.
+void reading_positions(const float *order, int nq, std::vector<int> &pos) {
+    std::vector<float> vote((size_t)nq, 0.0f);
+    for (int i = 0; i < nq; i++) {
+        const float *ri = order + (size_t)i * nq;
+        for (int j = 0; j < nq; j++)
+            if (j != i) vote[(size_t)j] += logistic(ri[j] - order[(size_t)j * nq + i]);
     }
+    std::vector<uint64_t> key((size_t)nq);
+    for (int j = 0; j < nq; j++) key[(size_t)j] = ((uint64_t)sortable_bits(vote[(size_t)j]) << 32) | (uint32_t)j;
+    std::sort(key.begin(), key.end());
+    pos.assign((size_t)nq, 0);
+    for (int r = 0; r < nq; r++) pos[(size_t)(uint32_t)key[(size_t)r]] = r;
+}
+
+// The k best of n scores, best first: higher score, then lower index.
+void best_scores(const float *score, int n, int k, std::vector<int32_t> &pick) {
+    std::vector<uint64_t> key((size_t)n);
+    for (int f = 0; f < n; f++) key[(size_t)f] = ((uint64_t)sortable_bits(score[f]) << 32) | (uint32_t)~(uint32_t)f;
+    std::nth_element(key.begin(), key.begin() + (k - 1), key.end(), std::greater<uint64_t>());
+    std::sort(key.begin(), key.begin() + k, std::greater<uint64_t>());
+    pick.resize((size_t)k);
+    for (int r = 0; r < k; r++) pick[(size_t)r] = (int32_t)~(uint32_t)key[(size_t)r];
+}
+
+// out rows r = 0..rows-1 get the NPIX mask bits of query qrow[r] as int32
+// 0/1, rows split over a few host threads
+void expand_mask_bits(const uint32_t *bits, const std::vector<int> &qrow, int32_t *out) {
+    constexpr int kWords = NPIX / 32;
+    const int rows = (int)qrow.size();
+    auto work = [&](int r0, int r1) {
+        for (int r = r0; r < r1; r++) {
+            const uint32_t *b = bits + (size_t)qrow[(size_t)r] * kWords;
+            int32_t *o = out + (size_t)r * NPIX;
+            for (int w = 0; w < kWords; w++, o += 32) {
+                const uint32_t v = b[w];
+                for (int t = 0; t < 32; t++) o[t] = (int32_t)((v >> t) & 1u);
+            }
+        }
+    };
+    const int nt = std::max(1, std::min<int>(8, (int)std::thread::hardware_concurrency()));
+    std::vector<std::thread> pool;
+    const int per = (rows + nt - 1) / nt;
+    for (int t = 1; t < nt && t * per < rows; t++) pool.emplace_back(work, t * per, std::min(rows, (t + 1) * per));
+    work(0, std::min(rows, per));
+    for (auto &th : pool) th.join();
+}
+
+void assemble_result(const HostOut &h, int ori_h, int ori_w, std::vector<float> &dets, std::vector<int32_t> &masks,
+                     std::vector<int32_t> &pick) {
+    std::vector<int> pos;
+    reading_positions(h.order, NQ, pos);
+    std::vector<float> score((size_t)NQ * NC);
+    for (size_t f = 0; f < score.size(); f++) score[f] = logistic(h.logits[f]);
+    best_scores(score.data(), NQ * NC, NQ, pick);
+    // the original size the boxes are restored to (sf = 800 / ori, then
+    // floor(800 / sf + 0.5))
+    const float sf_h = (float)IMG / (float)ori_h, sf_w = (float)IMG / (float)ori_w;
+    const float fh = std::floor((float)IMG / sf_h + 0.5f), fw = std::floor((float)IMG / sf_w + 0.5f);
+    dets.resize((size_t)NQ * 7);
+    std::vector<int> qrow((size_t)NQ);
+    for (int r = 0; r < NQ; r++) {
+        const int f = pick[(size_t)r], q = f / NC;
+        qrow[(size_t)r] = q;
+        const float cx = h.boxes[4 * q], cy = h.boxes[4 * q + 1], bw = h.boxes[4 * q + 2], bh = h.boxes[4 * q + 3];
+        float *row = dets.data() + (size_t)r * 7;
+        row[0] = (float)(f % NC);
+        row[1] = score[(size_t)f];
+        row[2] = (cx - bw * 0.5f) * fw;
+        row[3] = (cy - bh * 0.5f) * fh;
+        row[4] = (cx + bw * 0.5f) * fw;
+        row[5] = (cy + bh * 0.5f) * fh;
+        row[6] = (float)pos[(size_t)q];
+    }
+    masks.resize((size_t)NQ * NPIX);
+    expand_mask_bits(h.mbits, qrow, masks.data());
 }
 
 bool write_file(const std::string &path, const void *src, size_t nbytes) {
@@ -1072,28 +1146,32 @@ bool write_file(const std::string &path, const void *src, size_t nbytes) {
 
 struct ppdl_ctx {
     std::unique_ptr<ppdl::Net> net;
-    bool computed = false;
-    std::vector<float> out0, raw_logits, raw_boxes, raw_order, raw_masks;
-    std::vector<int32_t> out2, raw_sel;
+    bool computed = false;  // a replay has run (dumps, ppdl_get_raw)
+    bool fetched = false;   // `host` and the results belong to the last ppdl_infer
+    ppdl::HostOut host;     // pinned download buffers
+    void *pinned = nullptr;
+    std::vector<float> dets;
+    std::vector<int32_t> masks, picks;
+    ~ppdl_ctx() {
+        net.reset();
+        if (pinned) (void)hipHostFree(pinned);
+    }
+    // one pinned block for the four downloads
+    bool alloc_host() {
+        using namespace ppdl;
+        const size_t nl = (size_t)NQ * NC, nb = (size_t)NQ * 4, no = (size_t)NQ * NQ, nm = (size_t)NQ * (NPIX / 32);
+        if (hipHostMalloc(&pinned, (nl + nb + no + nm) * 4, hipHostMallocDefault) != hipSuccess) {
+            pinned = nullptr;
+            return false;
+        }
+        float *f = (float *)pinned;
+        host.logits = f;
+        host.boxes = f + nl;
+        host.order = f + nl + nb;
+        host.mbits = (uint32_t *)(f + nl + nb + no);
+        return true;
+    }
 };
-
-namespace {
-bool fetch(ppdl_ctx *c) {
-    using namespace ppdl;
-    c->raw_logits.resize((size_t)NQ * NC);
-    c->raw_boxes.resize((size_t)NQ * 4);
-    c->raw_order.resize((size_t)NQ * NQ);
-    c->raw_masks.resize((size_t)NQ * NPIX);
-    return hipMemcpy(c->raw_logits.data(), c->net->logits_, c->raw_logits.size() * 4, hipMemcpyDeviceToHost) ==
-               hipSuccess &&
-           hipMemcpy(c->raw_boxes.data(), c->net->boxes_, c->raw_boxes.size() * 4, hipMemcpyDeviceToHost) ==
-               hipSuccess &&
-           hipMemcpy(c->raw_order.data(), c->net->order_, c->raw_order.size() * 4, hipMemcpyDeviceToHost) ==
-               hipSuccess &&
-           hipMemcpy(c->raw_masks.data(), c->net->masks_, c->raw_masks.size() * 4, hipMemcpyDeviceToHost) ==
-               hipSuccess;
-}
-}  // namespace
 
 extern "C" PPDL_API ppdl_ctx *ppdl_init_ex(const char *model_path, int backend, int enable_dumps) {
     if (!model_path) return nullptr;
@@ -1125,6 +1203,12 @@ extern "C" PPDL_API ppdl_ctx *ppdl_init_ex(const char *model_path, int backend, 
         delete c;
         return nullptr;
     }
+    if (!c->alloc_host()) {
+        err = "pinned host allocation failed";
+        fprintf(stderr, "ppdl: %s\n", err.c_str());
+        delete c;
+        return nullptr;
+    }
     fprintf(stderr, "ppdl: loaded %s; graph of %d kernel launches\n", model_path, c->net->nodes());
     return c;
 }
@@ -1151,12 +1235,13 @@ extern "C" PPDL_API int ppdl_infer(ppdl_ctx *c, const float *image_chw, int ori_
     }
     const auto t1 = std::chrono::steady_clock::now();
     c->computed = true;
-    if (!fetch(c)) return 2;
-    ppdl::postprocess(c->raw_logits, c->raw_boxes, c->raw_order, c->raw_masks, ori_h, ori_w, c->out0, c->out2,
-                      c->raw_sel);
-    res->dets = c->out0.data();
+    c->fetched = false;
+    if (!c->net->download(c->host.logits, c->host.boxes, c->host.order, c->host.mbits)) return 2;
+    ppdl::assemble_result(c->host, ori_h, ori_w, c->dets, c->masks, c->picks);
+    c->fetched = true;
+    res->dets = c->dets.data();
     res->num_dets = ppdl::NQ;
-    res->masks = c->out2.data();
+    res->masks = c->masks.data();
     res->infer_ms = std::chrono::duration<double, std::milli>(t1 - t0).count();
     return 0;
 }
@@ -1194,15 +1279,17 @@ extern "C" PPDL_API int ppdl_dump(ppdl_ctx *c, const char *dir) {
 
 extern "C" PPDL_API int ppdl_dump_raw(ppdl_ctx *c, const char *pfx) {
     if (!c || !pfx) return 1;
-    if (!c->computed || c->raw_logits.empty()) {
+    if (!c->fetched) {
         fprintf(stderr, "ppdl: no inference to dump\n");
         return 1;
     }
+    using ppdl::NQ;
+    using ppdl::NC;
     const std::string p(pfx);
-    bool good = ppdl::write_file(p + "logits.bin", c->raw_logits.data(), c->raw_logits.size() * 4);
-    good = ppdl::write_file(p + "boxes.bin", c->raw_boxes.data(), c->raw_boxes.size() * 4) && good;
-    good = ppdl::write_file(p + "order.bin", c->raw_order.data(), c->raw_order.size() * 4) && good;
-    good = ppdl::write_file(p + "sel.bin", c->raw_sel.data(), c->raw_sel.size() * 4) && good;
+    bool good = ppdl::write_file(p + "logits.bin", c->host.logits, (size_t)NQ * NC * 4);
+    good = ppdl::write_file(p + "boxes.bin", c->host.boxes, (size_t)NQ * 4 * 4) && good;
+    good = ppdl::write_file(p + "order.bin", c->host.order, (size_t)NQ * NQ * 4) && good;
+    good = ppdl::write_file(p + "sel.bin", c->picks.data(), c->picks.size() * 4) && good;
     return good ? 0 : 1;
 }
 

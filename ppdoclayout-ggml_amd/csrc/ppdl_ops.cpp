@@ -8,7 +8,9 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <cstdio>
 #include <cstring>
+#include <string>
 #include <vector>
 
 #include "../../include/ppdl_hip_ops.h"
@@ -311,6 +313,17 @@ extern "C" PPDL_HIP_API int64_t ppdl_hip_workspace_bytes(const int32_t op_params
     bool im2col;
     if (!args_of_node(op_params, dst, src, &g, &im2col)) return 0;
     return gemm_ws_bytes_for(g, im2col);
+}
+
+extern "C" PPDL_HIP_API int ppdl_hip_kernel_name(const int32_t op_params[16], const ppdl_tview *dst,
+                                                 const ppdl_tview *src, int nsrc, char *buf, int cap) {
+    if (!buf || cap < 1 || check_node(op_params, dst, src, nsrc) != PPDL_OK) return -1;
+    GemmArgs g;
+    bool im2col;
+    std::string name;
+    if (args_of_node(op_params, dst, src, &g, &im2col)) name = gemm_kernel_name(g, ws_of(op_params, src, nsrc).bytes, im2col);
+    snprintf(buf, (size_t)cap, "%s", name.c_str());
+    return (int)name.size();
 }
 
 extern "C" PPDL_HIP_API int ppdl_hip_supports(const int32_t op_params[16], const ppdl_tview *dst,

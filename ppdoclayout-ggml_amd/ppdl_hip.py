@@ -43,6 +43,7 @@ EXPORTS = (
     "ppdl_hip_wg4_matrices",
     "ppdl_hip_workspace_bytes",
     "ppdl_hip_run_noalloc",
+    "ppdl_hip_kernel_name",
 )
 
 NOALLOC_SCRATCH_BYTES = 16 << 20  # PPDL_HIP_NOALLOC_SCRATCH_BYTES
@@ -85,6 +86,8 @@ def lib():
         L.ppdl_hip_run.restype = ctypes.c_int
         L.ppdl_hip_run_noalloc.argtypes = [i32p, tvp, tvp, ctypes.c_int, ctypes.c_void_p]
         L.ppdl_hip_run_noalloc.restype = ctypes.c_int
+        L.ppdl_hip_kernel_name.argtypes = [i32p, tvp, tvp, ctypes.c_int, ctypes.c_char_p, ctypes.c_int]
+        L.ppdl_hip_kernel_name.restype = ctypes.c_int
         L.ppdl_hip_im2col_f32.argtypes = [ctypes.c_void_p, ctypes.c_void_p] + [ctypes.c_int64] * 10 + [
             ctypes.c_int
         ] * 6 + [ctypes.c_void_p]
@@ -197,6 +200,16 @@ def workspace_bytes(op, dst, srcs, p14=0, p15=0):
     """Split-K workspace bytes the node's GEMM plan uses (0: none, -1: invalid node)."""
     d, arr, n = _views(dst, srcs)
     return lib().ppdl_hip_workspace_bytes(params(op, p14, p15), ctypes.byref(d), arr, n)
+
+
+def kernel_name(op, dst, srcs, p14=0, p15=0):
+    """Device kernel(s) ppdl_hip_run would launch for the node ('' for non-GEMM ops)."""
+    d, arr, n = _views(dst, srcs)
+    buf = ctypes.create_string_buffer(256)
+    rc = lib().ppdl_hip_kernel_name(params(op, p14, p15), ctypes.byref(d), arr, n, buf, 256)
+    if rc < 0:
+        raise PpdlError(f"ppdl_hip_kernel_name(op={op}): invalid node")
+    return buf.value.decode()
 
 
 def make_workspace(nbytes):

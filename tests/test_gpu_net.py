@@ -3,10 +3,13 @@ restatement of the reference's graph (oracle/ppdl_net.py).
 
 The model is the real architecture with seeded random weights written as a
 GGUF exactly as the reference's converter lays one out (no checkpoint can be
-fetched here); the input is a synthetic page.  Checks: every dumped
+fetched here).  Two inputs: a synthetic document page and seeded U(0,1)
+pixels (the stated benchmark input).  Checks per input: every dumped
 intermediate and raw output within a normwise tolerance, the top-300 encoder
-selection identical, the postprocessed detections through the reference's
-end-to-end gates (e2e_gates.py), and bit-identical graph replays.
+selection identical, the host result equal to the reference's postprocess
+restated on the GPU's own raw outputs, the postprocessed detections through
+the reference's end-to-end gates (e2e_gates.py), and bit-identical graph
+replays.
 """
 import os
 import sys
@@ -41,11 +44,12 @@ def model(tmp_path_factory):
     return path, weights
 
 
-@pytest.fixture(scope="module")
-def image():
-    from oracle import ppdl_net
+@pytest.fixture(scope="module", params=["document_page", "uniform_page"])
+def image(request):
+    import pages
 
-    return ppdl_net.doc_image(0)
+    say("input:", request.param)
+    return getattr(pages, request.param)(0)
 
 
 @pytest.fixture(scope="module")
@@ -142,6 +146,26 @@ def test_postprocessed_detections_pass_gates(gpu, cpu):
     say("e2e gates:", m)
     assert m["n_conf"] > 0
     assert e2e_gates.passes(m), m
+
+
+def test_host_result_equals_restated_postprocess(gpu, tmp_path):
+    """ppdl_infer's host result (mask bits packed on the device, key-based
+    selection and reading ranks on the host) against the oracle's
+    restatement of the reference postprocess (src/ppdoclayout.cpp:927-993)
+    applied to the same raw outputs: labels, boxes, ranks, the picked flat
+    indices and the masks bit for bit; scores to 2 ulp (host expf against
+    numpy's exp)."""
+    from oracle import ppdl_net
+
+    ctx, raw, _, dets, masks = gpu
+    d, m, sel = ppdl_net.postprocess(raw["logits"], raw["boxes"], raw["order"], raw["masks"], 1000, 700)
+    pfx = str(tmp_path / "run_")
+    assert ctx.dump_raw(pfx) == 0
+    assert np.array_equal(np.fromfile(pfx + "sel.bin", np.int32), sel)
+    cols = [0, 2, 3, 4, 5, 6]
+    assert np.array_equal(dets[:, cols], d[:, cols])
+    assert np.all(np.abs(dets[:, 1] - d[:, 1]) <= 2 * np.spacing(np.float32(1.0)))
+    assert np.array_equal(masks.reshape(300, -1), m)
 
 
 def test_result_contract(gpu):

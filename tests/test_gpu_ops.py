@@ -555,6 +555,31 @@ def test_msdeform_fixture_and_special_cases(hip, orc):
         assert normwise(hip_msdeform(hip, v2, o2, a2, r2), orc.msdeform(v2, o2, a2, r2)) < TOL
 
 
+def test_msdeform_skipped_corners_do_not_reach_the_sum(hip, orc):
+    """The reference skips a corner outside the map or with zero bilinear
+    weight (src/ppdoclayout.cpp:183), so a non-finite value there never
+    reaches the output.  Inf / NaN planted at token 0 (the address skipped
+    corners read) and at the zero-weight neighbours of a level-0 texel
+    centre: a query sampling only that centre, and a query whose samples all
+    fall outside, stay finite and equal the oracle."""
+    rng = np.random.default_rng(SEED + 45)
+    val = rng.standard_normal((13125, 256)).astype(np.float32)
+    val[0] = np.inf
+    val[3] = np.inf     # (x 3, y 0): weight 0 beside the centre of texel (2, 0)
+    val[102] = np.nan   # (x 2, y 1)
+    val[103] = -np.inf  # (x 3, y 1)
+    ref = np.array([[2.5 / 100, 0.5 / 100, 0.3, 0.3],  # texel centre (2, 0) of level 0
+                    [5.0, 5.0, 0.5, 0.5]], np.float32)  # every sample outside every level
+    off = np.zeros((2, 192), np.float32)
+    awr = rng.standard_normal((2, 96)).astype(np.float32)
+    y = hip_msdeform(hip, val, off, awr, ref)
+    oref = orc.msdeform(val, off, awr, ref)
+    assert np.isfinite(oref).all()
+    assert np.isfinite(y).all()
+    assert not y[1].any()
+    assert normwise(y, oref) < TOL
+
+
 # ---------------------------------------------------------------- mask box / top-k
 def test_mask_box(hip, orc):
     rng = np.random.default_rng(21)
@@ -612,11 +637,19 @@ def test_dma_tail_balancing_bit_identical(hip, orc, kind, IC, OC, H, W, monkeypa
     say(f"tail balancing {kind} {IC}->{OC} @{H}x{W}")
     rng = np.random.default_rng(IC + OC + W)
     outs = []
+    def launched(flag, op, dst, srcs, p14=0):
+        name = hip.kernel_name(op, dst, srcs, p14)
+        say(f"  PPDL_DMA_TAIL={flag}: {name}")
+        assert name.startswith("k_gemm_dma<64, 64, 2, false, 2, 2, ")
+        assert name.endswith("true>" if flag == "1" else "false>"), name
+
     if kind == "conv1x1":
         x, w, b = conv_inputs(rng, IC, H, W, OC, 1)
         for flag in ("1", "0"):
             monkeypatch.setenv("PPDL_DMA_TAIL", flag)
-            outs.append(host(hip_conv1x1(hip, x, w, b, 1)[0]))
+            out, srcs = hip_conv1x1(hip, x, w, b, 1)
+            launched(flag, hip.OP_CONV1X1_BA, out, list(srcs), 1)
+            outs.append(host(out))
         ref = orc.conv2d_ref(x, w, b, 1, 0, 1)
     else:
         T = W
@@ -625,7 +658,9 @@ def test_dma_tail_balancing_bit_identical(hip, orc, kind, IC, OC, H, W, monkeypa
         for flag in ("1", "0"):
             monkeypatch.setenv("PPDL_DMA_TAIL", flag)
             yt = torch.full((36, OC, T), float("nan"), device="cuda")
-            hip.run_checked(hip.OP_WG4_MADD, yt, with_ws(hip, hip.OP_WG4_MADD, yt, [dev(dt), dev(wg)]))
+            srcs = with_ws(hip, hip.OP_WG4_MADD, yt, [dev(dt), dev(wg)])
+            launched(flag, hip.OP_WG4_MADD, yt, srcs)
+            hip.run_checked(hip.OP_WG4_MADD, yt, srcs)
             outs.append(host(yt))
         ref = np.einsum("pko,pkt->pot", wg.astype(np.float64), dt.astype(np.float64))
     assert np.isfinite(outs[0]).all()
