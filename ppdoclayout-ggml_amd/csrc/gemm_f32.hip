@@ -64,7 +64,24 @@ struct SplitArgs {
     int splits;  // S (1 = no split)
     int ktiles_per_split;
     float *partials;  // S x batch x M x N
+    // block order: 1 = split-major (logical block = split * tiles + tile), so
+    // each XCD's contiguous range of blocks covers about 1/8 of the (split,
+    // tile) space and fetches one k range of A and B instead of every m row
+    // of A; 0 = tile-major (the S splits of a tile adjacent)
+    int split_major;
 };
+
+// (split, tile) of logical block `logical` of a split launch over `tiles`
+// output tiles
+__device__ __forceinline__ void split_of(const SplitArgs &sp, int logical, int tiles, int *split, int *tile) {
+    if (sp.split_major) {
+        *split = logical / tiles;
+        *tile = logical - *split * tiles;
+    } else {
+        *split = logical % sp.splits;
+        *tile = logical / sp.splits;
+    }
+}
 
 // Per-thread staging registers for one k tile.
 template <int EA, int EB4, int EB1>
@@ -222,9 +239,8 @@ __global__ __launch_bounds__(kThreads) void k_gemm(GemmArgs g, SplitArgs sp, int
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int logical = xcd_remap(blockIdx.x, gridDim.x);
-    const int S = SPLIT ? sp.splits : 1;
-    const int split = SPLIT ? logical % S : 0;
-    const int tile_id = SPLIT ? logical / S : logical;
+    int split = 0, tile_id = logical;
+    if (SPLIT) split_of(sp, logical, tiles_mn * g.batch, &split, &tile_id);
     const int bz = tile_id / tiles_mn;
     const int t = tile_id - bz * tiles_mn;
     const int tm = t % tiles_m, tn = t / tiles_m;
@@ -651,9 +667,8 @@ __global__ __launch_bounds__(kThreads * KG) void k_gemm_dma(GemmArgs g, SplitArg
         logical = xcd_remap(blockIdx.x, gridDim.x);
     }
     const bool active = !TAIL || half < 0 || wave < 4;  // wave-uniform
-    const int S = SPLIT ? sp.splits : 1;
-    const int split = SPLIT ? logical % S : 0;
-    const int tile_id = SPLIT ? logical / S : logical;
+    int split = 0, tile_id = logical;
+    if (SPLIT) split_of(sp, logical, tiles_mn * g.batch, &split, &tile_id);
     const int bz = tile_id / tiles_mn;
     const int t = tile_id - bz * tiles_mn;
     const int m0 = (t % tiles_m) * BM, n0 = (t / tiles_m) * BN;
@@ -1428,6 +1443,13 @@ int64_t tail_grid(int64_t T) {
     return any ? 8 * most : 0;
 }
 
+// Split launches order their blocks split-major (PPDL_SPLIT_ORDER=tile keeps
+// the S splits of a tile adjacent; read at every launch for A/B runs).
+int split_major_order() {
+    const char *e = getenv("PPDL_SPLIT_ORDER");
+    return (e && e[0] == 't') ? 0 : 1;
+}
+
 template <int BM, int BN, int WGM, bool SPLIT>
 void launch_dma(const GemmArgs &g, const SplitArgs &sp, int64_t total, int tiles_m, int tiles_n, hipStream_t s) {
     // 8 waves need at least one 16-byte copy per operand and wave
@@ -1459,10 +1481,11 @@ hipError_t launch(const GemmArgs &g, int S, const GemmWorkspace &ws, hipStream_t
     const int64_t a_ext = AMODE == 0 ? (int64_t)g.K * g.lda : (int64_t)g.M * g.lda;
     const int64_t b_ext = BMODE == 0 ? (int64_t)g.K * g.ldb : (int64_t)g.IC * g.IH * g.IW;  // im2col: the image
     if (a_ext + BM > 0x7fffffff || b_ext + BN > 0x7fffffff) return hipErrorInvalidValue;
-    SplitArgs sp{1, 0, nullptr};
+    SplitArgs sp{1, 0, nullptr, 0};
     if (S > 1) {
         const int nk = (g.K + kBK - 1) / kBK;
         sp.splits = S;
+        sp.split_major = split_major_order();
         sp.ktiles_per_split = (nk + S - 1) / S;
         sp.partials = (float *)ws.base;
         if (AMODE == 0 && BMODE == 0 && dma_ok(g))
