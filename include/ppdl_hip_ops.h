@@ -42,7 +42,8 @@ enum ppdl_op_id {
     PPDL_OP_TOPK          = 13, /* top-300 tokens by max-class logit            */
     PPDL_OP_CONV1X1_BA    = 14, /* ext: op 3 + op 5 fused (GEMM+bias+act)       */
     PPDL_OP_WG4_INPUT_PAD = 15, /* ext: op 10 reading the UNPADDED input        */
-    PPDL_OP_CONV_IM2COL   = 16  /* ext: implicit-im2col GEMM + bias + act       */
+    PPDL_OP_CONV_IM2COL   = 16, /* ext: implicit-im2col GEMM + bias + act       */
+    PPDL_OP_WG4_CONV      = 17  /* ext: ops 15 -> 12 -> 11 in one kernel        */
 };
 
 /* Activation codes (op 5 params[14], op 11 params[14]); same values as the
@@ -111,6 +112,9 @@ PPDL_HIP_API int ppdl_hip_supports(const int32_t op_params[16], const ppdl_tview
  *               extra zero pad after the last column and row (the
  *               reference's ggml_pad before its k2 convs); dst ne(OW,OH,OC),
  *               OW = (IW+2P+PE-K)/S+1.
+ *  17 WG4_CONV  the k3 s1 p1 conv of ops 15 -> 12 -> 11 as one kernel, no
+ *               dt / yt planes: src x ne(W,H,IC), wg4 ne(OC,IC,36), bias
+ *               ne(OC); params[14] = act, [15] = 0; dst ne(W,H,OC).
  *
  * Split-K workspace (ops 3, 12, 14, 16): one optional extra src after the
  * op's own (src[3] for 3/14/16, src[4] for 14 with an add, src[2] for 12),

@@ -1,5 +1,6 @@
-// Device-side scalar helpers shared by the kernels: the activation codes of
-// the GEMM / elementwise epilogues and the box-refinement inverse sigmoid.
+// Device-side helpers shared by the kernels: the activation codes of the GEMM
+// / elementwise epilogues, the box-refinement inverse sigmoid and the
+// XCD-aware block order.
 #pragma once
 #include <hip/hip_runtime.h>
 
@@ -23,6 +24,15 @@ __device__ __forceinline__ float inv_sigmoid(float x) {
     const float x1 = fminf(fmaxf(x, 1e-5f), 1.0f);
     const float x2 = fminf(fmaxf(1.0f - x, 1e-5f), 1.0f);
     return logf(x1) - logf(x2);
+}
+
+// Blocks are dispatched round-robin over the 8 XCDs (hardware id % 8).  The
+// logical block of hardware block `hw` out of `n`: each XCD gets a contiguous
+// range of logical blocks, so blocks sharing operands hit the same L2.
+__device__ __forceinline__ int xcd_remap(int hw, int n) {
+    const int q = n >> 3, r = n & 7;
+    const int xcd = hw & 7, slot = hw >> 3;
+    return xcd * q + (xcd < r ? xcd : r) + slot;
 }
 
 // box refinement (src/ppdoclayout.cpp:860-862): sigmoid(delta + inv_sigmoid(ref))

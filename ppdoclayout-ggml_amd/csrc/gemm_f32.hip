@@ -45,15 +45,6 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 constexpr int kThreads = 256;
 constexpr int kBK = 32;
 
-// Blocks are dispatched round-robin over the 8 XCDs (hardware id % 8).  Give
-// each XCD a contiguous range of logical tiles so that tiles sharing operands
-// (same n columns, same batch plane) hit the same L2.
-__device__ __forceinline__ int xcd_remap(int hw, int n) {
-    const int q = n >> 3, r = n & 7;
-    const int xcd = hw & 7, slot = hw >> 3;
-    return xcd * q + (xcd < r ? xcd : r) + slot;
-}
-
 __device__ __forceinline__ float4 ld4(const float *p) {
     float4 v;
     __builtin_memcpy(&v, p, 16);  // dword-aligned dwordx4 load

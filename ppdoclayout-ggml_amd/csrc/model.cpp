@@ -406,6 +406,21 @@ bool Net::concat_linears(GgufFile &g, const std::vector<std::string> &parts, con
     return true;
 }
 
+// k3 s1 p1 convs with at most 48 output channels on a large map run as the
+// fused Winograd kernel (op 17), the rest as the three-op pipeline 15 -> 12
+// -> 11.  Each op 17 block walks every input channel 4 at a time and
+// recomputes the input transform per 16-channel output tile, so it wins only
+// where the 3-op pipeline's plane traffic and launches dominate: in the
+// network graph 48 -> 48 @200 takes 26 us against 33.5; 96 -> 96 @100 (26.5
+// vs 24.8 us), 64 -> 64 @200 (52.9 vs 39.1) and every 256-channel conv (61 vs
+// 20-63 us in isolation) are faster as three ops.  PPDL_WG_FUSED=0 / 1 forces
+// either path for every k3 s1 p1 conv (read at graph build).
+bool wg_fused(int IC, int H, int W, int OC) {
+    if (const char *e = getenv("PPDL_WG_FUSED")) return e[0] == '1';
+    const int64_t T = (int64_t)((W + 3) / 4) * ((H + 3) / 4);
+    return IC <= 96 && OC <= 48 && T >= 625;
+}
+
 // ---------------------------------------------------------------------------
 // builder::conv (src/ppdoclayout.cpp:388-543): route by shape.
 Img Net::conv(const Img &x, const std::string &name, int s, int p, int act, float *out, int pad_end,
@@ -429,6 +444,19 @@ Img Net::conv(const Img &x, const std::string &name, int s, int p, int act, floa
         std::vector<ppdl_tview> src = {view(x), view(W(name + ".wr"), {OC, x.C, 1}), vb};
         if (add_mode) src.push_back(view(add, {OW, OH, OC}));
         tagged(name, PPDL_OP_CONV1X1_BA, act, add_mode, view(y), src);
+    } else if (K == 3 && s == 1 && p == 1 && pad_end == 0 && add_mode == 0 && wg_fused(x.C, x.H, x.W, OC)) {
+        // Winograd F(4,3) (:425-463) as one kernel (op 17): input transform,
+        // 36 plane products and output transform + bias + act, no planes in HBM
+        const size_t before = nodes_.size();
+        tagged(name, PPDL_OP_WG4_CONV, act, 0, view(y), {view(x), view(W(name + ".wg4"), {OC, x.C, 36}), vb});
+        if (nodes_.size() > before) {
+            Node &n = nodes_.back();
+            const double T = (double)((OW + 3) / 4) * ((OH + 3) / 4);
+            n.cls = 1;
+            n.flops = 2.0 * 36.0 * OC * T * x.C;  // the 36-plane contraction, as ops 12 would run it
+            n.bytes = 4.0 * ((double)x.C * x.H * x.W + 36.0 * x.C * OC + (double)OC * OH * OW);
+            n.kern = wg4_conv_kernel_name(x.C, x.H, x.W, OC);
+        }
     } else if (K == 3 && s == 1 && p == 1 && pad_end == 0 && add_mode == 0) {
         // Winograd F(4,3): pad fused into op 15, madd (op 12), output + bias + act (op 11) (:425-463)
         const int TW = (OW + 3) / 4, TH = (OH + 3) / 4, T = TW * TH;

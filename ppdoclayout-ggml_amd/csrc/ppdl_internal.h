@@ -127,6 +127,11 @@ hipError_t wg4_input(const float *x, float *dt, int IW, int IH, int IC, int TW, 
                      hipStream_t s);
 hipError_t wg4_output(const float *yt, const float *bias, float *out, int TW, int TH, int OC,
                       int OW, int OH, int act, int ldt, hipStream_t s);
+// the whole k3 s1 p1 conv in one kernel (op 17): x [IC][H][W], wg4
+// [36][IC][OC], out [OC][H][W] = act(conv + bias)
+hipError_t wg4_conv(const float *x, const float *wg4, const float *bias, float *out, int IC, int H, int W, int OC,
+                    int act, hipStream_t s);
+std::string wg4_conv_kernel_name(int IC, int H, int W, int OC);  // the instance the launch uses
 
 // ---- elementwise / data movement ----
 hipError_t bias_act(const float *in, const float *bias, float *out, int64_t n, int64_t plane,

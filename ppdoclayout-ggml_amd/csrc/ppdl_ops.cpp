@@ -186,6 +186,18 @@ int check_op(const int32_t *p, const ppdl_tview *dst, const ppdl_tview *src, int
             if (OW * OH > kMaxI32 || IC * K * K > kMaxI32 || IH * IW > kMaxI32) return PPDL_EINVAL;
             return PPDL_OK;
         }
+        case PPDL_OP_WG4_CONV: {
+            if (nsrc < 3) return PPDL_EINVAL;
+            const ppdl_tview *x = &src[0], *w = &src[1], *b = &src[2];
+            if (!contig_f32(dst) || !contig_f32(x) || !contig_f32(w) || !contig_f32(b)) return PPDL_EINVAL;
+            const int64_t W = x->ne[0], H = x->ne[1], IC = x->ne[2], OC = dst->ne[2];
+            if (x->ne[3] != 1 || !shape_is(dst, W, H, OC, 1) || !shape_is(w, OC, IC, 36, 1) || nelem(b) != OC)
+                return PPDL_EINVAL;
+            if (p[14] < 0 || p[14] > 2 || p[15] != 0) return PPDL_EINVAL;
+            const int64_t T = ((W + 3) / 4) * ((H + 3) / 4);
+            if (W * H * IC > kMaxI32 || 36 * IC * OC > kMaxI32 || T * ((OC + 15) / 16) > kMaxI32) return PPDL_EINVAL;
+            return PPDL_OK;
+        }
         case PPDL_OP_MSDEF: {
             if (nsrc < 4 || !contig_f32(dst)) return PPDL_EINVAL;
             // value, offsets and weights may be row-strided views (slices of
@@ -322,6 +334,8 @@ extern "C" PPDL_HIP_API int ppdl_hip_kernel_name(const int32_t op_params[16], co
     bool im2col;
     std::string name;
     if (args_of_node(op_params, dst, src, &g, &im2col)) name = gemm_kernel_name(g, ws_of(op_params, src, nsrc).bytes, im2col);
+    if (op_params[13] == PPDL_OP_WG4_CONV)
+        name = wg4_conv_kernel_name((int)src[0].ne[2], (int)src[0].ne[1], (int)src[0].ne[0], (int)dst->ne[2]);
     snprintf(buf, (size_t)cap, "%s", name.c_str());
     return (int)name.size();
 }
@@ -335,7 +349,7 @@ extern "C" PPDL_HIP_API int ppdl_hip_supports(const int32_t op_params[16], const
             case PPDL_OP_CONV: return (op_params[14] & 0xFF) == 1;
             case PPDL_OP_MASKBOX: case PPDL_OP_MSDEF: case PPDL_OP_BIASACT: case PPDL_OP_WG4_INPUT:
             case PPDL_OP_WG4_OUTPUT: case PPDL_OP_WG4_MADD: case PPDL_OP_TOPK: case PPDL_OP_CONV1X1_BA:
-            case PPDL_OP_WG4_INPUT_PAD: case PPDL_OP_CONV_IM2COL: return 1;
+            case PPDL_OP_WG4_INPUT_PAD: case PPDL_OP_CONV_IM2COL: case PPDL_OP_WG4_CONV: return 1;
             default: return 0;
         }
     }
@@ -369,6 +383,10 @@ int ppdl::run_node(const int32_t *p, const ppdl_tview *dst, const ppdl_tview *sr
                                         (float *)dst->data, (OW + 3) / 4, (OH + 3) / 4, OC, OW, OH,
                                         p[14], (int)(src[0].nb[1] / 4), s));
         }
+        case PPDL_OP_WG4_CONV:
+            return status_of(wg4_conv((const float *)src[0].data, (const float *)src[1].data, (const float *)src[2].data,
+                                      (float *)dst->data, (int)src[0].ne[2], (int)src[0].ne[1], (int)src[0].ne[0],
+                                      (int)dst->ne[2], p[14], s));
         case PPDL_OP_MSDEF:
             return status_of(msdeform((const float *)src[0].data, (int)(src[0].nb[1] / 4), (const float *)src[1].data,
                                       (int)(src[1].nb[1] / 4), (const float *)src[2].data, (int)(src[2].nb[1] / 4),

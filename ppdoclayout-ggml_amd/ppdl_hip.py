@@ -26,6 +26,7 @@ OP_TOPK = 13
 OP_CONV1X1_BA = 14
 OP_WG4_INPUT_PAD = 15
 OP_CONV_IM2COL = 16
+OP_WG4_CONV = 17
 
 ACT_NONE, ACT_RELU, ACT_SILU = 0, 1, 2
 

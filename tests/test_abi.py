@@ -38,7 +38,8 @@ def test_library_exports_every_declared_symbol(hip):
 
 def test_supports_id_only(hip):
     for op in (hip.OP_MSDEF, hip.OP_BIASACT, hip.OP_WG4_INPUT, hip.OP_WG4_OUTPUT, hip.OP_WG4_MADD,
-               hip.OP_MASKBOX, hip.OP_TOPK, hip.OP_CONV1X1_BA, hip.OP_WG4_INPUT_PAD, hip.OP_CONV_IM2COL):
+               hip.OP_MASKBOX, hip.OP_TOPK, hip.OP_CONV1X1_BA, hip.OP_WG4_INPUT_PAD, hip.OP_CONV_IM2COL,
+               hip.OP_WG4_CONV):
         assert hip.supports(op) == 1, op
     assert hip.supports(hip.OP_CONV, 1) == 1      # K=1 carried
     assert hip.supports(hip.OP_CONV, 3 | (1 << 8)) == 0  # legacy k3 tap-GEMM: not carried
@@ -78,6 +79,15 @@ def test_run_rejects_bad_nodes_without_launching(hip):
     assert hip.run(hip.OP_WG4_MADD, v([25, 8, 36]), [v([25, 16, 36]), v([8, 12, 36])], stream=0) == hip.EINVAL
     # winograd output: wrong TW param
     assert hip.run(hip.OP_WG4_OUTPUT, v([20, 20, 8]), [v([25, 8, 36]), v([8])], 0, 4, stream=0) == hip.EINVAL
+    # fused winograd conv: weight planes, bias length, act, params[15]
+    good17 = [v([20, 20, 8]), v([16, 8, 36]), v([16])]
+    assert hip.supports(hip.OP_WG4_CONV, 1, 0, v([20, 20, 16]), good17) == 1
+    assert hip.run(hip.OP_WG4_CONV, v([20, 20, 16]), [v([20, 20, 8]), v([16, 8, 16]), v([16])], 1, stream=0) == hip.EINVAL
+    assert hip.run(hip.OP_WG4_CONV, v([20, 20, 16]), [v([20, 20, 8]), v([16, 8, 36]), v([15])], 1, stream=0) == hip.EINVAL
+    assert hip.run(hip.OP_WG4_CONV, v([20, 20, 16]), good17, 3, stream=0) == hip.EINVAL
+    assert hip.run(hip.OP_WG4_CONV, v([20, 20, 16]), good17, 1, 1, stream=0) == hip.EINVAL
+    assert hip.run(hip.OP_WG4_CONV, v([20, 19, 16]), good17, 1, stream=0) == hip.EINVAL
+    assert hip.workspace_bytes(hip.OP_WG4_CONV, v([20, 20, 16]), good17, 1) == 0
     # im2col conv: dst shape inconsistent with K/S/P
     assert hip.run(hip.OP_CONV_IM2COL, v([50, 50, 8]), [v([100, 100, 4]), v([8, 4, 9]), v([8])],
                    3 | (1 << 8) | (1 << 16), stream=0) == hip.EINVAL

@@ -388,6 +388,64 @@ def test_conv_patch_kernel(hip, orc, IC, H, W, OC, K, S, P, PE, monkeypatch):
     assert normwise(outs[0], outs[1]) < TOL
 
 
+# ---------------------------------------------------------------- fused F(4,3) conv (op 17)
+def hip_wg4_conv(hip, x, w, b, act):
+    _, wg4 = hip.repack_conv(w)
+    out = torch.full((w.shape[0],) + x.shape[1:], float("nan"), device="cuda")
+    srcs = [dev(x), dev(wg4), dev(b)]
+    hip.run_checked(hip.OP_WG4_CONV, out, srcs, act)
+    return out, srcs
+
+
+@pytest.mark.parametrize("IC,H,W,OC", [
+    (256, 100, 100, 256), (256, 50, 50, 256), (256, 25, 25, 256), (48, 200, 200, 48), (96, 100, 100, 96),
+    (128, 100, 100, 96), (128, 200, 200, 64), (256, 100, 100, 64),
+    (1, 1, 1, 1), (3, 9, 10, 2), (5, 4, 4, 7), (17, 13, 11, 33), (33, 17, 23, 65), (64, 13, 200, 64),
+    (6, 3, 17, 20),
+])
+@pytest.mark.parametrize("act", [0, 2])
+def test_wg4_conv_fused(hip, orc, IC, H, W, OC, act):
+    """Op 17 (ops 15 -> 12 -> 11 as one kernel) on the Winograd benchmark sweep,
+    the network's other F(4,3) shapes and ragged edges (channels not a
+    multiple of 4 or 16, widths not a multiple of 4, tile counts not a
+    multiple of 16) against the oracle's reference CPU conv, the float64
+    truth, and the three-op pipeline."""
+    say(f"fused F(4,3) {IC}->{OC} @{H}x{W} act{act}")
+    rng = np.random.default_rng(IC * 5 + OC + H * 7 + W + act)
+    x, w, b = conv_inputs(rng, IC, H, W, OC, 3)
+    out, _ = hip_wg4_conv(hip, x, w, b, act)
+    y = host(out)
+    assert np.isfinite(y).all()
+    e = normwise(y, orc.conv2d_ref(x, w, b, 1, 1, act))
+    say(f"  normwise vs oracle {e:.2e}")
+    assert e < TOL
+    if IC * H * W * OC <= 40_000_000:
+        assert normwise(y, orc.conv2d_f64(x, w, b, 1, 1, act)) < TOL
+    three, _, _, _ = hip_winograd(hip, x, w, b, act)
+    assert normwise(y, host(three)) < TOL
+
+
+@pytest.mark.parametrize("ot", ["1", "2", "3", "4"])
+@pytest.mark.parametrize("IC,H,W,OC", [(17, 13, 11, 33), (96, 20, 24, 50), (256, 25, 25, 64), (4, 8, 8, 16),
+                                       (48, 40, 44, 48), (6, 9, 9, 20), (12, 10, 10, 16), (16, 10, 10, 16)])
+def test_wg4_conv_block_shapes(hip, orc, IC, H, W, OC, ot, monkeypatch):
+    """Every block shape of op 17 (1 to 4 tiles of 16 output channels), with
+    channel counts that leave partial tiles, blocks and steps, and step
+    counts below, at and above the prefetch depth: within the tolerance,
+    launched as named, and the same bits on a second run."""
+    monkeypatch.setenv("PPDL_WG_OT", ot)
+    say(f"fused F(4,3) {IC}->{OC} @{H}x{W} with {ot} channel tiles per block")
+    rng = np.random.default_rng(IC + OC + 7 * int(ot))
+    x, w, b = conv_inputs(rng, IC, H, W, OC, 3)
+    out, srcs = hip_wg4_conv(hip, x, w, b, 1)
+    assert hip.kernel_name(hip.OP_WG4_CONV, out, srcs, 1) == f"k_wg4_conv<{ot}>"
+    y = host(out).copy()
+    assert normwise(y, orc.conv2d_ref(x, w, b, 1, 1, 1)) < TOL
+    out.fill_(float("nan"))
+    hip.run_checked(hip.OP_WG4_CONV, out, srcs, 1)
+    assert np.array_equal(host(out), y)
+
+
 # ---------------------------------------------------------------- split-K
 SPLIT_SHAPES = [  # long K, few output tiles: the planner splits K
     ("conv1x1", (3328, 25, 25, 1024, 1, 1, 0)),
@@ -685,6 +743,7 @@ def test_ops_replay_under_graph_capture(hip):
     dt = torch.empty((36, 64, T), device="cuda")
     yt = torch.empty((36, 64, T), device="cuda")
     mid = torch.empty((64, 50, 50), device="cuda")
+    mid2 = torch.empty((64, 50, 50), device="cuda")
     out = torch.empty((32, 50, 50), device="cuda")
     val, off, awr, ref = msdef_300q(rng, 300)
     vt, ot, at, rt = dev(val), dev(off), dev(awr), dev(ref)
@@ -696,10 +755,11 @@ def test_ops_replay_under_graph_capture(hip):
         hip.run_checked(hip.OP_WG4_MADD, yt, [dt, wgt], stream=s)
         hip.run_checked(hip.OP_WG4_OUTPUT, mid, [yt, bt], 2, 13, stream=s)
         hip.run_checked(hip.OP_CONV1X1_BA, out, [mid, w1t, b1], 1, stream=s)
+        hip.run_checked(hip.OP_WG4_CONV, mid2, [xt, wgt, bt], 2, stream=s)
         hip.run_checked(hip.OP_MSDEF, ms, [vt, ot, at, rt], stream=s)
 
     seq()
-    eager_out, eager_ms = host(out).copy(), host(ms).copy()
+    eager_out, eager_ms, eager_mid2 = host(out).copy(), host(ms).copy(), host(mid2).copy()
     g = torch.cuda.CUDAGraph()
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
@@ -710,10 +770,12 @@ def test_ops_replay_under_graph_capture(hip):
     for i in range(3):
         out.zero_()
         ms.zero_()
+        mid2.zero_()
         g.replay()
         torch.cuda.synchronize()
         assert np.array_equal(host(out), eager_out), i
         assert np.array_equal(host(ms), eager_ms), i
+        assert np.array_equal(host(mid2), eager_mid2), i
         junk = torch.randn(1000, device="cuda").sum()  # eager work between replays
         torch.cuda.synchronize()
         del junk
