@@ -14,6 +14,13 @@ float64 sums where ggml uses ggml_float.
 
 Layouts: images (C, H, W); token tensors (tokens, 256); weights as the GGUF
 stores them in numpy order (conv OIHW, linear (out, in)).
+
+Composition pinned: backbone(), encoder() and decode() agree with
+transformers' PPDocLayoutV3 (an independent implementation of the network)
+evaluated in float64 on the same synthetic weights to <= 1e-5 normwise
+(tests/test_net_cpu.py against tests/golden/net_*.npz), with the reference's
+one deviation from it followed: the order head reads the pre-dec_norm
+hidden state (src/ppdoclayout.cpp:861-866).
 """
 import numpy as np
 
@@ -219,45 +226,67 @@ class Net:
             a = silu(self.conv(a, bp + ".c1", 1, 1, ACT_NONE) + self.conv(a, bp + ".c2", 1, 0, ACT_NONE))
         return a + self.conv(x, pfx + ".c2", 1, 0, ACT_SILU)
 
-    def encoder(self, x4, p8r, p16r, p32r, pos):
-        # :674-729
-        p8 = self.conv(p8r, "enc_in0", 1, 0, ACT_NONE)
-        p16 = self.conv(p16r, "enc_in1", 1, 0, ACT_NONE)
-        p32 = self.conv(p32r, "enc_in2", 1, 0, ACT_NONE)
-        s = p32.reshape(DM, -1).T.copy()  # to_seq: token = y*25 + x
+    def aifi(self, s, pos):
+        """The one AIFI encoder layer on tokens s (T, 256) with position
+        embedding pos (T, 256): post-norm attention + GELU FFN (:681-693)."""
         at = self.mha(s + pos, s, "aifi")
         s = self.ln(s + at, "aifi.ln1")
         ff = self.lin(gelu_erf(self.lin(s, "aifi.fc1")), "aifi.fc2")
-        s = self.ln(s + ff, "aifi.ln2")
-        p32 = s.T.reshape(DM, 25, 25).copy()
+        return self.ln(s + ff, "aifi.ln2")
+
+    def encoder(self, x4, p8r, p16r, p32r, pos=None):
+        """:674-729.  The reference fixes the 800x800 geometry (p32 25x25,
+        p16 50x50, p8 100x100, masks 200x200); every resize here is the 2x
+        step those sizes imply, so smaller maps follow the same graph."""
+        p8 = self.conv(p8r, "enc_in0", 1, 0, ACT_NONE)
+        p16 = self.conv(p16r, "enc_in1", 1, 0, ACT_NONE)
+        p32 = self.conv(p32r, "enc_in2", 1, 0, ACT_NONE)
+        h32, w32 = p32.shape[1:]
+        if pos is None:
+            pos = pos_embed(h32, w32)
+        s = p32.reshape(DM, -1).T.copy()  # to_seq: token = y*W + x
+        p32 = self.aifi(s, pos).T.reshape(DM, h32, w32).copy()
         self.dump("aifi", p32)
         lat0 = self.conv(p32, "lat0", 1, 0, ACT_SILU)
-        f16 = self.csp(np.concatenate([interp_nearest(lat0, 50, 50), p16], 0), "fpn0")
+        f16 = self.csp(np.concatenate([interp_nearest(lat0, 2 * h32, 2 * w32), p16], 0), "fpn0")
         lat1 = self.conv(f16, "lat1", 1, 0, ACT_SILU)
-        f8 = self.csp(np.concatenate([interp_nearest(lat1, 100, 100), p8], 0), "fpn1")
+        h16, w16 = f16.shape[1:]
+        f8 = self.csp(np.concatenate([interp_nearest(lat1, 2 * h16, 2 * w16), p8], 0), "fpn1")
         self.dump("f8", f8)
+        h8, w8 = f8.shape[1:]
         n16 = self.csp(np.concatenate([self.conv(f8, "pand0", 2, 1, ACT_SILU), lat1], 0), "pan0")
         self.dump("n16", n16)
         n32 = self.csp(np.concatenate([self.conv(n16, "pand1", 2, 1, ACT_SILU), lat0], 0), "pan1")
         self.dump("n32", n32)
         h0 = self.conv(f8, "mh0.0", 1, 1, ACT_SILU)
-        h1 = interp_bilinear(self.conv(n16, "mh1.0", 1, 1, ACT_SILU), 100, 100)
-        h2 = interp_bilinear(self.conv(n32, "mh2.0", 1, 1, ACT_SILU), 50, 50)
-        h2 = interp_bilinear(self.conv(h2, "mh2.2", 1, 1, ACT_SILU), 100, 100)
+        h1 = interp_bilinear(self.conv(n16, "mh1.0", 1, 1, ACT_SILU), h8, w8)
+        h2 = interp_bilinear(self.conv(n32, "mh2.0", 1, 1, ACT_SILU), h16, w16)
+        h2 = interp_bilinear(self.conv(h2, "mh2.2", 1, 1, ACT_SILU), h8, w8)
         mf = (h0 + h1) + h2
-        mf = interp_bilinear(self.conv(mf, "mh.out", 1, 1, ACT_SILU), 200, 200)
+        mf = interp_bilinear(self.conv(mf, "mh.out", 1, 1, ACT_SILU), 2 * h8, 2 * w8)
         mf = mf + self.conv(x4, "mlat", 1, 1, ACT_SILU)
         mf = self.conv(mf, "mout.base", 1, 1, ACT_SILU)
         mf = self.conv(mf, "mout.conv", 1, 0, ACT_NONE)
         self.dump("mask_feat", mf)
         return f8, n16, n32, mf
 
-    def forward(self, img):
-        """-> dict of raw outputs: logits (300, 25), boxes (300, 4), order
-        (300, 300) with [i][j] = q_i . k_j / 8, masks (300, 40000)."""
-        self.dumps = {}
-        x4, p8, p16, p32 = self.backbone(_f32(img))
-        f8, n16, n32, mf = self.encoder(x4, p8, p16, p32, pos_embed())
+    def decoder_layer(self, i, x, ref, source):
+        """Decoder layer i (:824-846): self-attention with the query
+        position MLP of ref, deformable cross-attention into source, FFN;
+        post-norm after each."""
+        dp = "dec%d" % i
+        qpos = self.lin(relu(self.lin(ref, "qpos.0")), "qpos.1")
+        x = self.ln(x + self.mha(x + qpos, x, dp + ".sa"), dp + ".ln1")
+        z = x + qpos
+        ca = K.msdeform(self.lin(source, dp + ".ca.vp"), self.lin(z, dp + ".ca.so"),
+                        self.lin(z, dp + ".ca.aw"), ref, nthreads=self.threads)
+        x = self.ln(x + self.lin(ca, dp + ".ca.op"), dp + ".ln2")
+        return self.ln(x + self.lin(relu(self.lin(x, dp + ".fc1")), dp + ".fc2"), dp + ".ln3")
+
+    def decode(self, f8, n16, n32, mf):
+        """Everything after the hybrid encoder (:733-882) at the 800x800
+        geometry: decoder inputs, query selection, mask-derived initial
+        boxes, six refining decoder layers and the heads."""
         mflat = mf.reshape(32, -1)  # (32, 40000)
         source = np.concatenate([self.conv(f, "dec_in%d" % i, 1, 0, ACT_NONE).reshape(DM, -1).T
                                  for i, f in enumerate((f8, n16, n32))], 0)
@@ -278,26 +307,31 @@ class Net:
         ref = sigmoid(refu)
         x = target
         for i in range(6):
-            dp = "dec%d" % i
-            qpos = self.lin(relu(self.lin(ref, "qpos.0")), "qpos.1")
-            x = self.ln(x + self.mha(x + qpos, x, dp + ".sa"), dp + ".ln1")
-            z = x + qpos
-            ca = K.msdeform(self.lin(source, dp + ".ca.vp"), self.lin(z, dp + ".ca.so"),
-                            self.lin(z, dp + ".ca.aw"), ref, nthreads=self.threads)
-            x = self.ln(x + self.lin(ca, dp + ".ca.op"), dp + ".ln2")
-            x = self.ln(x + self.lin(relu(self.lin(x, dp + ".fc1")), dp + ".fc2"), dp + ".ln3")
+            x = self.decoder_layer(i, x, ref, source)
             self.dump("hidden%d" % i, x)
             ref = sigmoid(self.mlp3(x, "bbox_head") + inv_sigmoid(ref))
         outq = self.ln(x, "dec_norm")
+        mq = self.mlp3(outq, "mq")
+        self.dump("mq", mq)
+        # the order head reads the last hidden state before dec_norm (:861-866)
         gp = self.lin(self.lin(x, "order5"), "gp")
+        self.dump("gp", gp)
         return {
             "logits": self.lin(outq, "score_head"),
             "boxes": ref,
-            "masks": _f32(self.mlp3(outq, "mq") @ mflat),
+            "masks": _f32(mq @ mflat),
             "order": _f32(gp[:, :64] @ gp[:, 64:].T) * np.float32(1.0 / 8.0),
             "topk": topk,
             "init_ref": refu,
         }
+
+    def forward(self, img):
+        """-> dict of raw outputs: logits (300, 25), boxes (300, 4), order
+        (300, 300) with [i][j] = q_i . k_j / 8, masks (300, 40000)."""
+        self.dumps = {}
+        x4, p8, p16, p32 = self.backbone(_f32(img))
+        f8, n16, n32, mf = self.encoder(x4, p8, p16, p32, pos_embed())
+        return self.decode(f8, n16, n32, mf)
 
 
 def inv_sigmoid(x):
@@ -308,12 +342,12 @@ def inv_sigmoid(x):
     return np.log(x1) - np.log(x2)
 
 
-def pos_embed():
-    """(625, 256) [sin_h | cos_h | sin_w | cos_w], float64 math (:887-903)."""
+def pos_embed(h=25, w=25):
+    """(h*w, 256) [sin_h | cos_h | sin_w | cos_w], float64 math (:887-903)."""
     omega = 1.0 / np.power(10000.0, np.arange(64) / 64.0)
-    h = np.repeat(np.arange(25), 25).astype(np.float64)[:, None]
-    w = np.tile(np.arange(25), 25).astype(np.float64)[:, None]
-    return np.concatenate([np.sin(h * omega), np.cos(h * omega), np.sin(w * omega), np.cos(w * omega)],
+    hh = np.repeat(np.arange(h), w).astype(np.float64)[:, None]
+    ww = np.tile(np.arange(w), h).astype(np.float64)[:, None]
+    return np.concatenate([np.sin(hh * omega), np.cos(hh * omega), np.sin(ww * omega), np.cos(ww * omega)],
                           1).astype(np.float32)
 
 

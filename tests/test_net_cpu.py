@@ -1,16 +1,26 @@
 """CPU checks of the full-network pieces: the GGUF layout, the synthetic
 model's tensor table, the stock-op restatements in oracle/ppdl_net.py
 (pinned against float64 closed forms, brute force and special cases), the
-postprocess, and the runtime library's file checks (no GPU needed)."""
+network composition of oracle/ppdl_net.py against transformers'
+PP-DocLayoutV3 run in float64 (tests/golden/net_*.npz, written by
+tests/golden/make_net_golden.py), the postprocess, and the runtime
+library's file checks (no GPU needed)."""
 import ctypes
 import os
 import struct
+import sys
 
 import numpy as np
 import pytest
 
 import synth_gguf as S
+from conftest import normwise
 from oracle import ppdl_net as N
+
+GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+if GOLD not in sys.path:
+    sys.path.insert(0, GOLD)
+import net_inputs as NI  # noqa: E402
 
 
 # ---------------------------------------------------------------- GGUF layout
@@ -212,6 +222,80 @@ def test_host_constants():
     # the 100x100 and 50x50 levels is invalid, the 25x25 level is all valid
     assert v.shape == (13125,) and int(v.sum()) == 13125 - (4 * 99) - (4 * 49)
     assert v[0] == 0 and v[101] == 1 and v[10000] == 0 and v[10051] == 1 and v[12500:].all()
+
+
+# ---------------------------------------------------------------- composition vs transformers
+# Each fixture holds float64 transformers outputs of the same synthetic model
+# (the GGUF weights with their BatchNorm fold undone); the oracle runs in
+# float32, so agreement is to float32 accumulation error: 1e-5 normwise.
+NET_TOL = 1e-5
+
+
+@pytest.fixture(scope="module")
+def fixture_net():
+    return N.Net(S.random_weights(NI.WEIGHT_SEED))
+
+
+def test_backbone_matches_transformers(fixture_net):
+    g = np.load(os.path.join(GOLD, "net_backbone.npz"))
+    outs = fixture_net.backbone(NI.backbone_input())
+    assert normwise(fixture_net.dumps["stem"], g["stem"]) <= NET_TOL
+    for i, o in enumerate(outs):
+        assert o.shape == g["st%d" % i].shape
+        assert normwise(o, g["st%d" % i]) <= NET_TOL, i
+
+
+def test_hybrid_encoder_matches_transformers(fixture_net):
+    g = np.load(os.path.join(GOLD, "net_encoder.npz"))
+    f8, n16, n32, mf = fixture_net.encoder(*NI.encoder_inputs())
+    got = {"aifi": fixture_net.dumps["aifi"], "f8": f8, "n16": n16, "n32": n32, "mask_feat": mf}
+    for k, v in got.items():
+        assert v.shape == g[k].shape, k
+        assert normwise(v, g[k]) <= NET_TOL, k
+
+
+def test_decoder_and_heads_match_transformers(fixture_net):
+    g = np.load(os.path.join(GOLD, "net_decode.npz"))
+    f8, n16, n32, mf = NI.decode_inputs()
+    o = fixture_net.decode(f8, n16, n32, mf)
+    d = fixture_net.dumps
+    assert np.array_equal(o["topk"], g["topk"])
+    # the mask-derived initial boxes cover whole-page, empty and local masks
+    ref = g["init_ref_unact"]
+    assert (ref[:, 2] < -11).sum() >= 10 and (ref[:, 2] > 11).sum() >= 10 and (np.abs(ref[:, 2]) < 5).sum() >= 50
+    assert normwise(o["init_ref"], ref) <= NET_TOL
+    for i in range(6):
+        assert normwise(d["hidden%d" % i][:32], g["hidden_first32"][i]) <= NET_TOL, i
+    assert normwise(o["logits"], g["logits"]) <= NET_TOL
+    assert normwise(o["boxes"], g["boxes"]) <= NET_TOL
+    # masks = mask queries x prototypes and order = q_i . k_j / sqrt(64),
+    # both from the stored head projections
+    mq, gp = g["mq"].astype(np.float64), g["gp"].astype(np.float64)
+    assert normwise(d["mq"], mq) <= NET_TOL and normwise(d["gp"], gp) <= NET_TOL
+    assert normwise(o["masks"], mq @ mf.reshape(32, -1).astype(np.float64)) <= NET_TOL
+    assert normwise(o["order"], gp[:, :64] @ gp[:, 64:].T / 8.0) <= NET_TOL
+
+
+def test_transformers_fixtures_catch_planted_mistakes(fixture_net):
+    """The fixtures separate the reference's composition from plausible
+    variants: the order head on the normed hidden state (what transformers
+    itself does), and a swapped residual / norm order in the AIFI layer."""
+    g = np.load(os.path.join(GOLD, "net_decode.npz"))
+    o = fixture_net.decode(*NI.decode_inputs())
+    x = fixture_net.dumps["hidden5"]
+    gp_post = fixture_net.lin(fixture_net.lin(fixture_net.ln(x, "dec_norm"), "order5"), "gp")
+    assert normwise(gp_post, g["gp"]) > 1e-2 and normwise(o["order"], g["gp"][:, :64] @ g["gp"][:, 64:].T / 8) <= NET_TOL
+
+    class PreNormAifi(N.Net):
+        def aifi(self, s, pos):
+            h = self.ln(s, "aifi.ln1")
+            s = s + self.mha(h + pos, h, "aifi")
+            return s + self.lin(N.gelu_erf(self.lin(self.ln(s, "aifi.ln2"), "aifi.fc1")), "aifi.fc2")
+
+    ge = np.load(os.path.join(GOLD, "net_encoder.npz"))
+    bad = PreNormAifi(fixture_net.w)
+    bad.encoder(*NI.encoder_inputs())
+    assert normwise(bad.dumps["aifi"], ge["aifi"]) > 1e-2
 
 
 # ---------------------------------------------------------------- postprocess
