@@ -14,9 +14,6 @@
 namespace ppdl {
 namespace {
 
-__constant__ int kLvlW[3] = {100, 50, 25};
-__constant__ int kLvlStart[3] = {0, 10000, 12500};
-
 // ---------------------------------------------------------------------------
 // MSDeformAttn: one 256-thread block per query; wave w serves heads 2w, 2w+1
 // (lane>>5 picks the head, lane&31 the channel).  For a fixed (head, point,
@@ -26,79 +23,92 @@ __constant__ int kLvlStart[3] = {0, 10000, 12500};
 //   awr  (NQ, 96) pre-softmax [h*12 + l*4 + p]   ref (NQ, 4) cxcywh
 // val, off and awr rows may be strided (ldv, ldo, ldw floats): slices of a
 // wider projection.
+//
+// The sampling arithmetic is the same for the 32 lanes of a head, so it is
+// done once per sample: lane j < 12 of a head owns sample j = l*4 + p (its
+// logit, its offset pair, its 4 corners) and publishes the corners' tokens
+// and weights in LDS; then every lane reads its head's 48 (token, weight)
+// pairs as broadcasts, issues the 48 gathers together and accumulates in
+// the reference's l -> p -> corner order.  The softmax max is a shuffle
+// reduction (exact in any order); its sum adds the 12 terms in index order,
+// as the reference does.
+struct MsCorner {
+    int tok;   // -1: the corner is skipped
+    float wv;  // attention weight x bilinear weight
+};
+
 __global__ __launch_bounds__(256) void k_msdeform(const float *__restrict__ val,
                                                   const float *__restrict__ off,
                                                   const float *__restrict__ awr,
                                                   const float *__restrict__ ref,
                                                   float *__restrict__ out, int nq, int ldv, int ldo,
                                                   int ldw) {
+    constexpr int kS = 3 * 4 * 4;
+    __shared__ __attribute__((aligned(16))) MsCorner corners[8][kS];
     const int q = blockIdx.x;
-    if (q >= nq) return;
+    if (q >= nq) return;  // the whole block, before any barrier
     const int h = threadIdx.x >> 5, c = threadIdx.x & 31;
-    const float rx = ref[q * 4 + 0], ry = ref[q * 4 + 1];
-    const float rw = ref[q * 4 + 2], rh = ref[q * 4 + 3];
+    const int j = min(c, 11);  // this lane's sample (lanes 12-31 shadow sample 11)
 
-    const float *a = awr + (int64_t)q * ldw + h * 12;
-    float w[12];
-    float amax = a[0];
+    const float a = awr[(int64_t)q * ldw + h * 12 + j];
+    float amax = c < 12 ? a : -INFINITY;
 #pragma unroll
-    for (int i = 1; i < 12; i++) amax = fmaxf(amax, a[i]);
+    for (int m = 1; m < 32; m <<= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 32));
+    const float e = expf(a - amax);
     float wsum = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 12; i++) {
-        w[i] = expf(a[i] - amax);
-        wsum += w[i];
-    }
-#pragma unroll
-    for (int i = 0; i < 12; i++) w[i] /= wsum;
+    for (int i = 0; i < 12; i++) wsum += __shfl(e, i, 32);  // lane i of this head's 32
+    const float wt = e / wsum;
 
-    const float *o = off + (int64_t)q * ldo + h * 24;
-    const float *vh = val + h * kHD + c;
-    // Corner tokens and weights first, the 48 gathers next (all issued
-    // together), the accumulation last in the reference's l -> p -> corner
-    // order.  A corner outside the map or with zero bilinear weight is
-    // skipped, as the reference skips it: its gather reads token 0 (any valid
-    // address) and a select, not a multiply by zero, leaves the sum as it was,
-    // so a non-finite value there cannot reach the output.
-    constexpr int kS = 3 * 4 * 4;
-    float wv[kS];
-    int tok[kS];
-    bool use[kS];
+    if (c < 12) {
+        const int l = j >> 2;
+        const int W = l == 0 ? 100 : l == 1 ? 50 : 25, H = W;
+        const int st = l == 0 ? 0 : l == 1 ? 10000 : 12500;
+        const float rx = ref[q * 4 + 0], ry = ref[q * 4 + 1];
+        const float rw = ref[q * 4 + 2], rh = ref[q * 4 + 3];
+        const float *o = off + (int64_t)q * ldo + h * 24 + j * 2;
+        const float lx = rx + o[0] / 4.0f * rw * 0.5f;
+        const float ly = ry + o[1] / 4.0f * rh * 0.5f;
+        // grid_sample bilinear, zero padding, align_corners = false.  The
+        // clamp only keeps the float->int conversion defined: any sample
+        // beyond it has both corner columns (rows) outside the map.
+        const float fx = fminf(fmaxf(lx * (float)W - 0.5f, -2.0f), (float)W + 1.0f);
+        const float fy = fminf(fmaxf(ly * (float)H - 0.5f, -2.0f), (float)H + 1.0f);
+        const int x0 = (int)floorf(fx), y0 = (int)floorf(fy);
+        const float tx = fx - (float)x0, ty = fy - (float)y0;
+        const float cw[4] = {(1.0f - tx) * (1.0f - ty), tx * (1.0f - ty), (1.0f - tx) * ty, tx * ty};
 #pragma unroll
-    for (int l = 0; l < 3; l++) {
-        const int W = kLvlW[l], H = kLvlW[l], st = kLvlStart[l];
-#pragma unroll
-        for (int p = 0; p < 4; p++) {
-            const float ox = o[(l * 4 + p) * 2 + 0];
-            const float oy = o[(l * 4 + p) * 2 + 1];
-            const float lx = rx + ox / 4.0f * rw * 0.5f;
-            const float ly = ry + oy / 4.0f * rh * 0.5f;
-            // grid_sample bilinear, zero padding, align_corners = false.  The
-            // clamp only keeps the float->int conversion defined: any sample
-            // beyond it has both corner columns (rows) outside the map.
-            const float fx = fminf(fmaxf(lx * (float)W - 0.5f, -2.0f), (float)W + 1.0f);
-            const float fy = fminf(fmaxf(ly * (float)H - 0.5f, -2.0f), (float)H + 1.0f);
-            const int x0 = (int)floorf(fx), y0 = (int)floorf(fy);
-            const float tx = fx - (float)x0, ty = fy - (float)y0;
-            const float wt = w[l * 4 + p];
-            const float cw[4] = {(1.0f - tx) * (1.0f - ty), tx * (1.0f - ty), (1.0f - tx) * ty, tx * ty};
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-                const int xx = x0 + (k & 1), yy = y0 + (k >> 1);
-                const bool in = xx >= 0 && xx < W && yy >= 0 && yy < H && cw[k] != 0.0f;
-                const int i = (l * 4 + p) * 4 + k;
-                use[i] = in;
-                wv[i] = wt * cw[k];
-                tok[i] = in ? st + yy * W + xx : 0;
-            }
+        for (int k = 0; k < 4; k++) {
+            // a corner outside the map or with zero bilinear weight is
+            // skipped, as the reference skips it
+            const int xx = x0 + (k & 1), yy = y0 + (k >> 1);
+            const bool in = xx >= 0 && xx < W && yy >= 0 && yy < H && cw[k] != 0.0f;
+            corners[h][j * 4 + k] = MsCorner{in ? st + yy * W + xx : -1, wt * cw[k]};
         }
+    }
+    __syncthreads();
+
+    // A skipped corner's gather reads token 0 (any valid address) and a
+    // select, not a multiply by zero, leaves the sum as it was, so a
+    // non-finite value there cannot reach the output.
+    const float *vh = val + h * kHD + c;
+    const int4 *cp = reinterpret_cast<const int4 *>(corners[h]);
+    int tok[kS];
+    float wv[kS];
+#pragma unroll
+    for (int i = 0; i < kS / 2; i++) {
+        const int4 t = cp[i];
+        tok[2 * i] = t.x;
+        wv[2 * i] = __int_as_float(t.y);
+        tok[2 * i + 1] = t.z;
+        wv[2 * i + 1] = __int_as_float(t.w);
     }
     float v[kS];
 #pragma unroll
-    for (int i = 0; i < kS; i++) v[i] = vh[(int64_t)tok[i] * ldv];
+    for (int i = 0; i < kS; i++) v[i] = vh[(int64_t)max(tok[i], 0) * ldv];
     float acc = 0.0f;
 #pragma unroll
-    for (int i = 0; i < kS; i++) acc = use[i] ? fmaf(wv[i], v[i], acc) : acc;
+    for (int i = 0; i < kS; i++) acc = tok[i] >= 0 ? fmaf(wv[i], v[i], acc) : acc;
     out[(int64_t)q * kDM + h * kHD + c] = acc;
 }
 

@@ -1100,6 +1100,105 @@ hipError_t launch_frag(const GemmArgs &g, hipStream_t s) {
     return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------
+// Direct VALU conv for k3 s2 convs with at most 4 input and 32 output
+// channels (the first stem conv, 3 -> 32 at 800 -> 400).  At 27 products per
+// output it is bound by its output writes (20 MB) and by FMA latency, not by
+// the MFMA rate.  A block owns 64 consecutive output pixels (lane = pixel, so
+// each store is 256 contiguous bytes) and all 32 output channels; each of its
+// two waves computes 16 channels as 16 independent FMA chains over the
+// pixel's 3 x 3 x IC window, held in registers.  The weights are staged in
+// LDS transposed to one padded row per output channel (read as broadcast
+// float4s) from a coalesced read of the .wr rows.
+__device__ float kZeroWord = 0.0f;  // read-only in practice: global, not constant, so loads stay global_load
+
+template <int IC>
+__global__ __launch_bounds__(128) void k_conv_k3s2(GemmArgs g) {
+    constexpr int KK = 9 * IC, KP = (KK + 3) & ~3, MG = 16;
+    __shared__ __attribute__((aligned(16))) float ws[32 * KP];
+    __shared__ float bs[32];
+    const int M = g.M, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t lda = (uint32_t)g.lda;
+    for (int i = tid; i < 32 * KP; i += 128) {
+        const int k = i >> 5, m = i & 31;
+        ws[m * KP + k] = (m < M && k < KK) ? g.A[(uint32_t)k * lda + (uint32_t)m] : 0.0f;
+    }
+    if (tid < 32) bs[tid] = (g.bias && tid < M) ? g.bias[tid] : 0.0f;
+    __syncthreads();
+
+    const int n = blockIdx.x * 64 + lane;
+    if (n >= g.N) return;
+    const int OW = g.OW, IH = g.IH, IW = g.IW;
+    const int oy = n / OW, ox = n - oy * OW;
+    const int iy0 = 2 * oy - g.P, ix0 = 2 * ox - g.P;
+    const uint32_t plane = (uint32_t)IH * (uint32_t)IW;
+    const float *__restrict__ X = g.B;
+    float v[KP];
+#pragma unroll
+    for (int kh = 0; kh < 3; kh++)
+#pragma unroll
+        for (int kw = 0; kw < 3; kw++)
+#pragma unroll
+            for (int ic = 0; ic < IC; ic++) {
+                // an out-of-bounds tap reads a zero word: the choice is made
+                // on the address, so every load is issued unconditionally (a
+                // select on the loaded value let the compiler branch around
+                // each load and wait for it)
+                const int iy = iy0 + kh, ix = ix0 + kw;
+                const bool ok = iy >= 0 && iy < IH && ix >= 0 && ix < IW;
+                v[(kh * 3 + kw) * IC + ic] =
+                    *(ok ? X + (uint32_t)ic * plane + (uint32_t)iy * (uint32_t)IW + (uint32_t)ix : &kZeroWord);
+            }
+#pragma unroll
+    for (int k = KK; k < KP; k++) v[k] = 0.0f;
+
+    const int m0 = wave * MG;
+    float a[MG];
+#pragma unroll
+    for (int j = 0; j < MG; j++) a[j] = bs[m0 + j];
+    // one k quad of the 16 channels' weights at a time (a fully unrolled
+    // loop kept every weight in registers: 256 VGPRs, one wave per SIMD)
+#pragma unroll 1
+    for (int q = 0; q < KP / 4; q++)
+#pragma unroll
+        for (int j = 0; j < MG; j++) {
+            const float4 w4 = reinterpret_cast<const float4 *>(ws + (m0 + j) * KP)[q];
+            a[j] = fmaf(w4.x, v[4 * q], a[j]);
+            a[j] = fmaf(w4.y, v[4 * q + 1], a[j]);
+            a[j] = fmaf(w4.z, v[4 * q + 2], a[j]);
+            a[j] = fmaf(w4.w, v[4 * q + 3], a[j]);
+        }
+    float *__restrict__ C = g.C;
+    const uint32_t ldc = (uint32_t)g.ldc;
+#pragma unroll
+    for (int j = 0; j < MG; j++)
+        if (m0 + j < M) C[(uint32_t)(m0 + j) * ldc + (uint32_t)n] = act_f(a[j], g.act);
+}
+
+// The direct kernel serves op 16 for k3 s2 convs with IC <= 4 and OC <= 32
+// (plain bias + act into a CHW output).  PPDL_CONV_DIRECT=0 turns it off.
+bool direct_ok(const GemmArgs &g) {
+    const char *e = getenv("PPDL_CONV_DIRECT");  // read per call: tests switch it
+    const bool off = e && e[0] == '0';
+    return !off && g.KW == 3 && g.S == 2 && g.IC >= 1 && g.IC <= 4 && g.M >= 1 && g.M <= 32 && !g.a_rowmajor &&
+           !g.c_trans && g.add_mode == 0 && !g.add && g.batch == 1 && g.N >= 1 && g.OW >= 1 && g.N % g.OW == 0 &&
+           (int64_t)g.IC * g.IH * g.IW < (1LL << 31) && (int64_t)9 * g.IC * g.lda + 32 < (1LL << 31) &&
+           (int64_t)32 * g.ldc + g.N < (1LL << 31);
+}
+
+hipError_t launch_direct(const GemmArgs &g, hipStream_t s) {
+    const int64_t blocks = ((int64_t)g.N + 63) / 64;
+    if (blocks > 0x7fffffff) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)blocks);
+    switch (g.IC) {
+        case 1: hipLaunchKernelGGL(k_conv_k3s2<1>, grid, dim3(128), 0, s, g); break;
+        case 2: hipLaunchKernelGGL(k_conv_k3s2<2>, grid, dim3(128), 0, s, g); break;
+        case 3: hipLaunchKernelGGL(k_conv_k3s2<3>, grid, dim3(128), 0, s, g); break;
+        default: hipLaunchKernelGGL(k_conv_k3s2<4>, grid, dim3(128), 0, s, g); break;
+    }
+    return hipGetLastError();
+}
+
 // Split-K fix-up: the GEMM epilogue applied to sum_{s=0..S-1} P[s], s
 // ascending.  Partials are [s][batch][M][N]; VEC = 4 needs a plain C with
 // ldc == N (four consecutive n share m).
@@ -1533,6 +1632,7 @@ hipError_t dispatch(const GemmArgs &g_in, const GemmWorkspace &ws, hipStream_t s
     g.n_vec = BMODE == 0 ? n_vec_of(g) : 0;
     if (BMODE == 1) {
         if (const int cc = patch_cc(g)) return launch_patch(g, cc, s);
+        if (direct_ok(g)) return launch_direct(g, s);
         if (frag_ok(g)) return launch_frag(g, s);
     }
     if (g.a_w4) {
@@ -1606,7 +1706,7 @@ GemmPlan gemm_plan(const GemmArgs &g, int64_t ws_bytes, bool im2col) {
 
 int64_t gemm_ws_bytes_for(const GemmArgs &g, bool im2col) {
     if (g.a_w4) return 0;  // the small kernel, no split-K
-    if (im2col && !patch_cc(g) && frag_ok(g)) return 0;  // the fragment kernel splits K inside a block
+    if (im2col && !patch_cc(g) && (direct_ok(g) || frag_ok(g))) return 0;  // neither kernel uses a workspace
     const GemmPlan p = gemm_plan(g, INT64_MAX, im2col);
     return gemm_ws_bytes(g.M, g.N, g.batch, p.cfg, p.splits);
 }
@@ -1615,6 +1715,7 @@ hipError_t gemm_dense(const GemmArgs &g, const GemmWorkspace &ws, hipStream_t s)
 
 std::string gemm_kernel_name(const GemmArgs &g, int64_t ws_bytes, bool im2col) {
     if (im2col && patch_cc(g)) return g.KW == 3 ? "k_conv_patch<3, 2>" : "k_conv_patch<2, 1>";
+    if (im2col && direct_ok(g)) return "k_conv_k3s2<" + std::to_string(g.IC) + ">";
     if (im2col && frag_ok(g)) return "k_conv_frag<" + std::to_string(frag_waves(g)) + ">";
     if (g.a_w4) return "k_gemm_small<2, " + std::to_string(small_waves(g.K, small_tiles(g))) + ", false>";
     const GemmPlan p = gemm_plan(g, ws_bytes, im2col);

@@ -327,6 +327,33 @@ def test_conv_im2col_shapes(hip, orc, IC, IH, IW, OC, K, S, P):
     assert normwise(y, orc.conv2d_f64(x, w, b, S, P, 1)) < TOL
 
 
+@pytest.mark.parametrize("IC,IH,IW,OC,P", [(3, 800, 800, 32, 1), (3, 9, 7, 5, 1), (1, 5, 5, 32, 1), (4, 17, 33, 17, 0),
+                                         (2, 3, 3, 1, 1), (3, 2, 1, 32, 1), (4, 6, 11, 30, 1)])
+@pytest.mark.parametrize("act", [0, 1])
+def test_conv_direct_kernel(hip, orc, IC, IH, IW, OC, P, act, monkeypatch):
+    """Op 16 k3 s2 with IC <= 4 and OC <= 32 (the first stem conv) runs the
+    direct VALU kernel: against float64, and against the MFMA fragment
+    kernel it replaced (PPDL_CONV_DIRECT=0), odd widths included (the last
+    pair's second pixel is not stored)."""
+    say(f"direct conv k3s2p{P} {IC}->{OC} @{IH}x{IW} act{act}")
+    rng = np.random.default_rng(IC * 7 + IH + IW + OC + act)
+    x, w, b = conv_inputs(rng, IC, IH, IW, OC, 3)
+    wr, _ = hip.repack_conv(w)
+    OH, OW = (IH + 2 * P - 3) // 2 + 1, (IW + 2 * P - 3) // 2 + 1
+    p14 = 3 | (2 << 8) | (P << 16) | (act << 24)
+    outs = []
+    for flag, kern in (("1", f"k_conv_k3s2<{IC}>"), ("0", "k_conv_frag<")):
+        monkeypatch.setenv("PPDL_CONV_DIRECT", flag)
+        out = torch.full((OC, OH, OW), float("nan"), device="cuda")
+        srcs = [dev(x), dev(wr), dev(b)]
+        assert hip.kernel_name(hip.OP_CONV_IM2COL, out, srcs, p14).startswith(kern)
+        hip.run_checked(hip.OP_CONV_IM2COL, out, srcs, p14)
+        outs.append(host(out))
+    ref = orc.conv2d_f64(x, w, b, 2, P, act)
+    assert np.isfinite(outs[0]).all()
+    assert normwise(outs[0], ref) < TOL and normwise(outs[1], ref) < TOL
+
+
 @pytest.mark.parametrize("IC,IH,IW,K,S,P", [(48, 401, 401, 2, 1, 0), (256, 100, 100, 3, 2, 1), (3, 800, 800, 3, 2, 1),
                                             (5, 7, 9, 3, 1, 1), (16, 10, 10, 1, 1, 0), (2, 3, 3, 3, 2, 1)])
 def test_im2col_ggml_layout(hip, orc, IC, IH, IW, K, S, P):
