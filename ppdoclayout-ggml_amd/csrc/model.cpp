@@ -41,6 +41,8 @@ constexpr int IMG = 800, NQ = 300, NC = 25, NTOK = kNTOK, NPIX = kMaskPix;
 struct Img {
     float *d = nullptr;
     int C = 0, H = 0, W = 0;
+    int64_t ld = 0;  // channel-plane stride in floats; 0: H * W (packed planes)
+    int64_t plane() const { return ld ? ld : (int64_t)H * W; }
 };
 struct Seq {
     float *d = nullptr;
@@ -85,7 +87,12 @@ ppdl_tview view(const void *d, std::vector<int64_t> ne, int32_t type = PPDL_TYPE
     v.type = type;
     return v;
 }
-ppdl_tview view(const Img &x) { return view(x.d, {x.W, x.H, x.C}); }
+ppdl_tview view(const Img &x) {
+    ppdl_tview v = view(x.d, {x.W, x.H, x.C});
+    v.nb[2] = x.plane() * 4;
+    v.nb[3] = v.nb[2] * x.C;
+    return v;
+}
 
 // Winograd planes ne(T, C, 36) with rows padded to ldt tiles
 ppdl_tview planes(const float *d, int64_t T, int64_t C, int64_t ldt) {
@@ -271,8 +278,10 @@ class Net {
     static int ok(hipError_t e) { return e == hipSuccess ? 0 : 3; }
 
     // ---- layers ----
+    // out_ld: channel-plane stride of the output (0: packed); depthwise and
+    // 1x1 convs only, like a strided x
     Img conv(const Img &x, const std::string &name, int s, int p, int act, float *out = nullptr, int pad_end = 0,
-             const float *add = nullptr, int add_mode = 0);
+             const float *add = nullptr, int add_mode = 0, int64_t out_ld = 0);
     Seq lin(const Seq &x, const std::string &name, int act, float *out = nullptr, const float *add = nullptr,
             int add_mode = 0, const float *a_add = nullptr, int a_add_n = 0);
     Seq ln(const Seq &a, const float *b, const std::string &name, float *out = nullptr, int out_chw = 0);
@@ -424,20 +433,26 @@ bool wg_fused(int IC, int H, int W, int OC) {
 // ---------------------------------------------------------------------------
 // builder::conv (src/ppdoclayout.cpp:388-543): route by shape.
 Img Net::conv(const Img &x, const std::string &name, int s, int p, int act, float *out, int pad_end,
-              const float *add, int add_mode) {
+              const float *add, int add_mode, int64_t out_ld) {
     const auto &ne = shape(name + ".weight");  // (K, K, IC, OC)
     const int K = (int)ne[0], ICw = (int)ne[2], OC = (int)ne[3];
     const float *b = W(name + ".bias");
     const int OH = (x.H + 2 * p + pad_end - K) / s + 1, OW = (x.W + 2 * p + pad_end - K) / s + 1;
-    Img y{out ? out : alloc((int64_t)OC * OH * OW), OC, OH, OW};
+    const int64_t ypl = out_ld ? out_ld : (int64_t)OH * OW;
+    Img y{out ? out : alloc((int64_t)OC * ypl), OC, OH, OW, out_ld};
     if (ICw == 1 && x.C != 1) {
         // depthwise: ggml_conv_2d_dw_direct + bias + act (:400-404)
         const float *w = W(name + ".weight");
         const Img xi = x;
-        node(name, 1, [=](hipStream_t st) { return ok(dwconv(xi.d, w, b, y.d, xi.C, xi.H, xi.W, K, s, p, act, st)); });
+        node(name, 1, [=](hipStream_t st) {
+            return ok(dwconv(xi.d, w, b, y.d, xi.C, xi.H, xi.W, K, s, p, act, xi.plane(), y.plane(), st));
+        });
         return y;
     }
     if (ICw != x.C && bad_node_.empty()) bad_node_ = name + " (channel mismatch)";
+    // plane-strided maps exist for the 1x1 GEMMs only (ops 3 / 14 take them)
+    if ((x.ld || out_ld) && !(K == 1 && s == 1 && p == 0 && pad_end == 0) && bad_node_.empty())
+        bad_node_ = name + " (plane-strided map into a conv other than 1x1)";
     const ppdl_tview vb = view(b, {OC});
     if (K == 1 && s == 1 && p == 0 && pad_end == 0) {
         // op 3 + op 5 fused: one GEMM writing CHW with bias/act (:408-423)
@@ -601,20 +616,22 @@ Seq Net::mha(const Seq &x, const float *pos, const std::string &pfx, float *out,
 // `cin` channels; each layer writes its output into the next slice.
 void Net::hg_block(const Img &cat, int cin, const std::string &pfx, bool light, int mid, Img *y, float *out,
                    const float *resid) {
-    Img cur{cat.d, cin, cat.H, cat.W};
-    const int64_t plane = (int64_t)cat.H * cat.W;
+    // a plane-strided concat (light blocks only) keeps its stride through the
+    // layers' slots and the aggregation's middle map
+    Img cur{cat.d, cin, cat.H, cat.W, cat.ld};
+    const int64_t plane = cat.plane();
     for (int l = 0; l < 6; l++) {
         const std::string lp = pfx + ".l" + std::to_string(l);
         float *slot = cat.d + (cin + (int64_t)l * mid) * plane;
         if (light) {
             Img t = conv(cur, lp + ".c1", 1, 0, kActNone);
-            cur = conv(t, lp + ".c2", 1, 2, kActRelu, slot);  // depthwise k5 p2
+            cur = conv(t, lp + ".c2", 1, 2, kActRelu, slot, 0, nullptr, 0, cat.ld);  // depthwise k5 p2
         } else {
             cur = conv(cur, lp, 1, 1, kActRelu, slot);  // k3 p1
         }
     }
-    Img full{cat.d, cin + 6 * mid, cat.H, cat.W};
-    Img a = conv(full, pfx + ".agg0", 1, 0, kActRelu);
+    Img full{cat.d, cin + 6 * mid, cat.H, cat.W, cat.ld};
+    Img a = conv(full, pfx + ".agg0", 1, 0, kActRelu, nullptr, 0, nullptr, 0, cat.ld);
     *y = conv(a, pfx + ".agg1", 1, 0, kActRelu, out, 0, resid, resid ? 2 : 0);
 }
 
@@ -679,8 +696,12 @@ bool Net::build(bool dumps, std::string *err) {
     hg_block(cat_b1, 1024, "st2.b1", true, 192, &t, cat_b2.d, cat_b1.d);       // + residual
     hg_block(cat_b2, 1024, "st2.b2", true, 192, &s2, nullptr, cat_b2.d);       // + residual
     dump("st2", s2);
-    Img cat_s3{alloc((1024 + 6 * 384LL) * 625), 1024 + 6 * 384, 25, 25};
-    conv(s2, "st3.ds", 2, 1, kActNone, cat_s3.d);  // dw -> 25, 1024
+    // The 25x25 maps of stage 3 keep a 628-float plane stride (625 rounded
+    // up to whole float4s), so the aggregation GEMMs' B rows are 16-byte
+    // aligned and take the direct-to-LDS loader.
+    const int64_t ld25 = 628;
+    Img cat_s3{alloc((1024 + 6 * 384LL) * ld25), 1024 + 6 * 384, 25, 25, ld25};
+    conv(s2, "st3.ds", 2, 1, kActNone, cat_s3.d, 0, nullptr, 0, ld25);  // dw -> 25, 1024
     hg_block(cat_s3, 1024, "st3.b0", true, 384, &s3, nullptr, nullptr);  // 25, 2048
     dump("st3", s3);
 

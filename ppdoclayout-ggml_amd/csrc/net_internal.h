@@ -5,9 +5,10 @@
 
 namespace ppdl {
 
-// depthwise conv, w [C][K][K], out [C][OH][OW], + bias + act
+// depthwise conv, w [C][K][K], out [C][OH][OW], + bias + act; x planes
+// in_plane floats apart (>= IH*IW), out planes out_plane apart (>= OH*OW)
 hipError_t dwconv(const float *x, const float *w, const float *b, float *out, int C, int IH, int IW, int K, int S,
-                  int P, int act, hipStream_t s);
+                  int P, int act, int64_t in_plane, int64_t out_plane, hipStream_t s);
 // 2x2 s1 max pool over x zero-padded at the right/bottom; out keeps [C][H][W]
 hipError_t maxpool2_padend(const float *x, float *out, int C, int H, int W, hipStream_t s);
 // out = interp(x) (+ add): nearest (bilinear = 0) or half-pixel bilinear

@@ -27,13 +27,14 @@ constexpr int kDwLds = 8192;  // floats of staged input per block
 template <int K>
 __global__ __launch_bounds__(256) void k_dwconv(const float *__restrict__ x, const float *__restrict__ w,
                                                 const float *__restrict__ b, float *__restrict__ out, int C,
-                                                int IH, int IW, int OH, int OW, int S, int P, int act, int RB) {
+                                                int IH, int IW, int OH, int OW, int S, int P, int act, int RB,
+                                                int64_t in_plane, int64_t out_plane) {
     __shared__ float tile[kDwLds];
     const int c = blockIdx.y, oy0 = blockIdx.x * RB;
     const int rows = min(RB, OH - oy0);
     const int TR = (rows - 1) * S + K, TC = IW + 2 * P;  // staged rows / columns
     const int iy0 = oy0 * S - P;
-    const float *__restrict__ xc = x + (int64_t)c * IH * IW;
+    const float *__restrict__ xc = x + (int64_t)c * in_plane;
     for (int i = threadIdx.x; i < TR * TC; i += 256) {
         const int r = i / TC, col = i - r * TC;
         const int iy = iy0 + r, ix = col - P;
@@ -45,7 +46,7 @@ __global__ __launch_bounds__(256) void k_dwconv(const float *__restrict__ x, con
 #pragma unroll
     for (int i = 0; i < K * K; i++) wk[i] = wc[i];
     const float bc = b[c];
-    float *__restrict__ oc = out + (int64_t)c * OH * OW + (int64_t)oy0 * OW;
+    float *__restrict__ oc = out + (int64_t)c * out_plane + (int64_t)oy0 * OW;
     for (int o = threadIdx.x; o < rows * OW; o += 256) {
         const int oy = o / OW, ox = o - oy * OW;
         const float *t = tile + oy * S * TC + ox * S;
@@ -448,19 +449,23 @@ hipError_t mask_bits(const float *ml, uint32_t *bits, int nq, int npix, hipStrea
 }
 
 hipError_t dwconv(const float *x, const float *w, const float *b, float *out, int C, int IH, int IW, int K, int S,
-                  int P, int act, hipStream_t s) {
+                  int P, int act, int64_t in_plane, int64_t out_plane, hipStream_t s) {
     const int OH = (IH + 2 * P - K) / S + 1, OW = (IW + 2 * P - K) / S + 1;
     const int TC = IW + 2 * P;
     // the band's staged rows must fit the LDS tile: (RB - 1) * S + K rows of TC
     const int max_rows = kDwLds / TC;
-    if (C < 1 || OH < 1 || OW < 1 || C > 65535 || max_rows < K || (K != 3 && K != 5)) return hipErrorInvalidValue;
+    if (C < 1 || OH < 1 || OW < 1 || C > 65535 || max_rows < K || (K != 3 && K != 5) ||
+        in_plane < (int64_t)IH * IW || out_plane < (int64_t)OH * OW)
+        return hipErrorInvalidValue;
     const int bands = std::max(1, (2048 + C - 1) / C);
     const int RB = std::max(1, std::min((OH + bands - 1) / bands, (max_rows - K) / S + 1));
     const dim3 grid((OH + RB - 1) / RB, C);
     if (K == 3)
-        hipLaunchKernelGGL(k_dwconv<3>, grid, dim3(256), 0, s, x, w, b, out, C, IH, IW, OH, OW, S, P, act, RB);
+        hipLaunchKernelGGL(k_dwconv<3>, grid, dim3(256), 0, s, x, w, b, out, C, IH, IW, OH, OW, S, P, act, RB,
+                           in_plane, out_plane);
     else
-        hipLaunchKernelGGL(k_dwconv<5>, grid, dim3(256), 0, s, x, w, b, out, C, IH, IW, OH, OW, S, P, act, RB);
+        hipLaunchKernelGGL(k_dwconv<5>, grid, dim3(256), 0, s, x, w, b, out, C, IH, IW, OH, OW, S, P, act, RB,
+                           in_plane, out_plane);
     return hipGetLastError();
 }
 

@@ -30,6 +30,17 @@ bool contig_f32(const ppdl_tview *t) {
     return true;
 }
 
+// F32 CHW map ne(W, H, C, 1) with packed rows and planes at any stride
+// nb[2] >= 4*W*H (a multiple of 4 bytes): a contiguous map or a view whose
+// channel planes are padded
+bool chw_f32(const ppdl_tview *t) {
+    if (!t || !t->data || t->type != PPDL_TYPE_F32 || t->nb[0] != 4) return false;
+    for (int i = 0; i < 4; i++)
+        if (t->ne[i] < 1) return false;
+    if (t->ne[3] != 1 || t->nb[1] != 4 * t->ne[0] || t->nb[2] < t->nb[1] * t->ne[1] || t->nb[2] % 4 != 0) return false;
+    return (t->nb[2] / 4) * t->ne[2] <= ((int64_t)1 << 40);
+}
+
 bool contig_i32(const ppdl_tview *t) {
     if (!t || !t->data || t->type != PPDL_TYPE_I32 || t->nb[0] != 4) return false;
     for (int i = 0; i < 4; i++)
@@ -104,14 +115,19 @@ int check_conv1x1(const int32_t *p, const ppdl_tview *dst, const ppdl_tview *src
                   bool fused) {
     if (nsrc < (fused ? 3 : 2)) return PPDL_EINVAL;
     const ppdl_tview *x = &src[0], *w = &src[1];
-    if (!contig_f32(dst) || !contig_f32(x) || !contig_f32(w)) return PPDL_EINVAL;
+    // x and dst: CHW maps whose channel planes may be padded (nb[2] >= 4*W*H)
+    if (!chw_f32(dst) || !chw_f32(x) || !contig_f32(w)) return PPDL_EINVAL;
     const int64_t W = x->ne[0], H = x->ne[1], IC = x->ne[2], OC = dst->ne[2];
-    if (x->ne[3] != 1 || !shape_is(dst, W, H, OC, 1) || !shape_is(w, OC, IC, 1, 1)) return PPDL_EINVAL;
+    if (!shape_is(dst, W, H, OC, 1) || !shape_is(w, OC, IC, 1, 1)) return PPDL_EINVAL;
     if (W * H > kMaxI32 || IC > kMaxI32 || OC > kMaxI32) return PPDL_EINVAL;
+    // the GEMM indexes planes with 32-bit element offsets
+    if ((x->nb[2] / 4) * IC > kMaxI32 || (dst->nb[2] / 4) * OC > kMaxI32) return PPDL_EINVAL;
     if (fused) {
         if (!contig_f32(&src[2]) || nelem(&src[2]) != OC) return PPDL_EINVAL;
         if (p[14] < 0 || p[14] > 2 || p[15] < 0 || p[15] > 2) return PPDL_EINVAL;
-        if (p[15] && (nsrc < 4 || !contig_f32(&src[3]) || !shape_is(&src[3], W, H, OC, 1))) return PPDL_EINVAL;
+        // the added map is laid out as dst
+        if (p[15] && (nsrc < 4 || !chw_f32(&src[3]) || !shape_is(&src[3], W, H, OC, 1) || src[3].nb[2] != dst->nb[2]))
+            return PPDL_EINVAL;
     }
     return PPDL_OK;
 }
@@ -245,9 +261,9 @@ bool args_of_node(const int32_t *p, const ppdl_tview *dst, const ppdl_tview *src
             g->A = (const float *)w->data;
             g->lda = dst->ne[2];
             g->B = (const float *)x->data;
-            g->ldb = x->ne[0] * x->ne[1];
+            g->ldb = x->nb[2] / 4;  // channel-plane strides (packed: W*H)
             g->C = (float *)dst->data;
-            g->ldc = dst->ne[0] * dst->ne[1];
+            g->ldc = dst->nb[2] / 4;
             g->bias = fused ? (const float *)src[2].data : nullptr;
             g->M = (int)dst->ne[2];
             g->N = (int)(x->ne[0] * x->ne[1]);

@@ -155,6 +155,19 @@ def raw_view(ptr, ne, ty=TYPE_F32):
     return v
 
 
+def chw_view(t, W, H):
+    """ppdl_tview ne(W, H, C) of a contiguous (C, ld) tensor whose rows are
+    channel planes of W*H values padded to ld (plane stride nb[2] = 4*ld)."""
+    v = view(t)
+    C, ld = t.shape
+    if ld < W * H:
+        raise PpdlError("plane stride below W*H")
+    v.ne[0], v.ne[1], v.ne[2], v.ne[3] = W, H, C, 1
+    v.nb[0], v.nb[1], v.nb[2] = 4, 4 * W, 4 * ld
+    v.nb[3] = v.nb[2] * C
+    return v
+
+
 def _views(dst, srcs):
     d = dst if isinstance(dst, TView) else view(dst)
     s = [x if isinstance(x, TView) else view(x) for x in srcs]

@@ -112,6 +112,30 @@ def test_supports_with_views_uses_the_same_validation(hip):
     assert hip.supports(hip.OP_CONV1X1_BA, 1, 0, v([10, 10, 9]), good[1]) == 0
 
 
+def test_conv1x1_accepts_plane_strided_maps(hip):
+    """Ops 3 / 14 take CHW maps whose channel planes are padded (nb[2] >
+    4*W*H, rows packed); an added map must share dst's layout."""
+    def pv(W, H, C, ld):
+        t = hip.raw_view(FAKE, [W, H, C])
+        t.nb[2] = 4 * ld
+        t.nb[3] = t.nb[2] * C
+        return t
+    w, b = hip.raw_view(FAKE, [8, 16, 1]), hip.raw_view(FAKE, [8])
+    assert hip.supports(hip.OP_CONV1X1_BA, 1, 0, pv(25, 25, 8, 628), [pv(25, 25, 16, 628), w, b]) == 1
+    assert hip.supports(hip.OP_CONV, 1, 0, pv(25, 25, 8, 628), [pv(25, 25, 16, 625), w]) == 1
+    assert hip.supports(hip.OP_CONV1X1_BA, 1, 2, pv(25, 25, 8, 628), [pv(25, 25, 16, 628), w, b, pv(25, 25, 8, 628)]) == 1
+    # the added map laid out differently from dst
+    assert hip.supports(hip.OP_CONV1X1_BA, 1, 2, pv(25, 25, 8, 628), [pv(25, 25, 16, 628), w, b, pv(25, 25, 8, 625)]) == 0
+    # planes overlapping (stride below W*H), padded rows, odd byte strides
+    assert hip.supports(hip.OP_CONV1X1_BA, 1, 0, pv(25, 25, 8, 624), [pv(25, 25, 16, 628), w, b]) == 0
+    bad = pv(25, 25, 16, 700)
+    bad.nb[1] = 104
+    assert hip.supports(hip.OP_CONV1X1_BA, 1, 0, pv(25, 25, 8, 628), [bad, w, b]) == 0
+    odd = pv(25, 25, 16, 628)
+    odd.nb[2] = 4 * 628 + 2
+    assert hip.supports(hip.OP_CONV1X1_BA, 1, 0, pv(25, 25, 8, 628), [odd, w, b]) == 0
+
+
 def test_im2col_rejects_out_of_range_args(hip):
     assert hip.im2col_f32(FAKE, FAKE, 8, 8, 8, 8, 3, 3, 4, 1, 64, 256, 0, 1, 1, 1, 1, 1, stream=0) == 0
     assert hip.im2col_f32(0, FAKE, 8, 8, 8, 8, 3, 3, 4, 1, 64, 256, 1, 1, 1, 1, 1, 1, stream=0) == 0

@@ -175,6 +175,38 @@ def test_conv1x1_shapes(hip, orc, IC, H, W, OC, act):
     assert normwise(y, orc.conv2d_f64(x, w, b, 1, 0, act)) < TOL
 
 
+@pytest.mark.parametrize("IC,H,W,OC,ld", [(3328, 25, 25, 1024, 628), (1024, 25, 25, 2048, 628), (40, 5, 7, 12, 37),
+                                          (384, 25, 25, 384, 640)])
+def test_conv1x1_plane_strided(hip, orc, IC, H, W, OC, ld):
+    """Op 14 on maps whose channel planes are ld floats apart (the 25x25
+    maps of stage 3 use 628 so that GEMM B rows are whole float4s): the
+    result equals the packed-map conv, with and without an added map, and
+    the padding columns of dst stay untouched.  With ld % 4 == 0 the
+    stage-3 aggregation GEMMs take the direct-to-LDS loader."""
+    say(f"1x1 plane-strided {IC}->{OC} @{H}x{W} ld {ld}")
+    rng = np.random.default_rng(IC + OC + ld)
+    x, w, b = conv_inputs(rng, IC, H, W, OC, 1)
+    wr, _ = hip.repack_conv(w)
+    P = H * W
+    xs = torch.full((IC, ld), float("nan"), device="cuda")
+    xs[:, :P] = dev(x.reshape(IC, P))
+    add = rng.standard_normal((OC, P)).astype(np.float32)
+    adds = torch.full((OC, ld), float("nan"), device="cuda")
+    adds[:, :P] = dev(add)
+    ref = orc.conv2d_ref(x, w, b, 1, 0, 1).reshape(OC, P)
+    for mode in (0, 2):
+        out = torch.full((OC, ld), float("nan"), device="cuda")
+        srcs = [hip.chw_view(xs, W, H), dev(wr), dev(b)] + ([hip.chw_view(adds, W, H)] if mode else [])
+        d = hip.chw_view(out, W, H)
+        srcs = with_ws(hip, hip.OP_CONV1X1_BA, d, srcs, 1, mode, True)
+        if ld % 4 == 0 and IC >= 1024:  # the stage-3 aggregations (smaller GEMMs plan the small kernel)
+            assert hip.kernel_name(hip.OP_CONV1X1_BA, d, srcs, 1, mode).startswith("k_gemm_dma")
+        hip.run_checked(hip.OP_CONV1X1_BA, d, srcs, 1, mode)
+        y = host(out)
+        assert np.isnan(y[:, P:]).all()
+        assert normwise(y[:, :P], ref + add if mode else ref) < TOL
+
+
 @pytest.mark.parametrize("wv", ["", "1", "2", "4", "8", "16"])
 @pytest.mark.parametrize("IC,H,W,OC", [
     (1, 1, 1, 1), (3, 7, 5, 2), (17, 13, 11, 33), (256, 15, 20, 256), (1024, 17, 19, 96), (70, 9, 9, 300),
