@@ -88,7 +88,10 @@ PPDL_HIP_API int ppdl_hip_supports(const int32_t op_params[16], const ppdl_tview
  *               offsets and logits may be row-strided (nb[1] >= 4*ne[0]).
  *  3  CONV      src: x ne(W,H,IC), wr ne(OC,IC,1), bias ne(OC) (unused);
  *               params[14] = K | pad<<8 with K=1, pad=0; params[15] = 0
- *               (CHW out); dst ne(W,H,OC) = sum_ic x*wr, no bias.
+ *               (CHW out); dst ne(W,H,OC) = sum_ic x*wr, no bias.  x and
+ *               dst may have padded channel planes (nb[1] = 4W, nb[2] >=
+ *               4WH, a multiple of 4): an extension, the reference passes
+ *               contiguous maps.
  *  5  BIASACT   src: in (any 4-d, contiguous), bias ne(ne2 of dst);
  *               params[14] = act; dst = act(in + bias[i / (ne0*ne1)]).
  *  10 WG4_INPUT src: padded x ne(IWp,IHp,IC) with IWp >= 4*TW+2,
@@ -104,7 +107,8 @@ PPDL_HIP_API int ppdl_hip_supports(const int32_t op_params[16], const ppdl_tview
  *               lower index.
  *  14 CONV1X1_BA as op 3 plus bias/act: params[14] = act; params[15] = add
  *               mode: 0 none, 1 dst = act(conv + bias + src[3]), 2 dst =
- *               act(conv + bias) + src[3]; src[3] has dst's shape.
+ *               act(conv + bias) + src[3]; src[3] has dst's shape and
+ *               strides.
  *  15 WG4_INPUT_PAD as op 10 but src is the unpadded x ne(W,H,IC) and the
  *               conv's zero pad of 1 is applied while reading.
  *  16 CONV_IM2COL src: x ne(IW,IH,IC), wr ne(OC,IC,K*K), bias ne(OC);
