@@ -136,6 +136,7 @@ class Net {
     }
 
     bool load(const std::string &path, std::string *err);
+    bool fold_repvgg(GgufFile &g, const std::string &bp, std::string *err);
     bool concat_linears(GgufFile &g, const std::vector<std::string> &parts, const std::string &name,
                         std::string *err);
     bool build(bool dumps, std::string *err);
@@ -375,10 +376,49 @@ bool Net::load(const std::string &path, std::string *err) {
         for (int i = 0; i < 6; i++) vp.push_back("dec" + std::to_string(i) + ".ca.vp");
         if (!concat_linears(g, vp, "dec.ca.vp", err)) return false;
     }
+    for (const std::string blk : {"fpn0", "fpn1", "pan0", "pan1"})
+        for (int i = 0; i < 3; i++)
+            if (!fold_repvgg(g, blk + ".bn" + std::to_string(i), err)) return false;
     if (oom_) {
         *err = "device allocation failed";
         return false;
     }
+    return true;
+}
+
+// RepVGG block bp (src/ppdoclayout.cpp:656-660): silu(c1_3x3(a) + c2_1x1(a))
+// is one 3x3 conv whose centre tap carries both branches, w = c1.w with
+// w[oc][ic][1][1] += c2.w[oc][ic], bias c1.b + c2.b: the same sums
+// regrouped, so the block becomes a single Winograd conv and its 1x1 GEMM
+// disappears.  Stored as bp.rep (.wr, .wg4, .bias, shape); skipped (the
+// graph keeps the two convs) when a part is absent or the shapes differ.
+bool Net::fold_repvgg(GgufFile &g, const std::string &bp, std::string *err) {
+    const std::string c1 = bp + ".c1", c2 = bp + ".c2";
+    for (const auto &n : {c1 + ".weight", c1 + ".bias", c2 + ".weight", c2 + ".bias"})
+        if (!g.index.count(n)) return true;
+    const auto &t1 = g.tensors[g.index[c1 + ".weight"]], &t2 = g.tensors[g.index[c2 + ".weight"]];
+    if (t1.ne.size() != 4 || t2.ne.size() != 4 || t1.ne[0] != 3 || t1.ne[1] != 3 || t2.ne[0] != 1 || t2.ne[1] != 1 ||
+        t1.ne[2] != t2.ne[2] || t1.ne[3] != t2.ne[3])
+        return true;
+    const int64_t IC = t1.ne[2], OC = t1.ne[3];
+    std::vector<float> w((size_t)(9 * IC * OC)), w2((size_t)(IC * OC)), b1((size_t)OC), b2((size_t)OC);
+    if (!gguf_read_f32(g, t1, w.data(), err) || !gguf_read_f32(g, t2, w2.data(), err) ||
+        !gguf_read_f32(g, g.tensors[g.index[c1 + ".bias"]], b1.data(), err) ||
+        !gguf_read_f32(g, g.tensors[g.index[c2 + ".bias"]], b2.data(), err))
+        return false;
+    for (int64_t o = 0; o < OC; o++) {
+        for (int64_t i = 0; i < IC; i++) w[(size_t)((o * IC + i) * 9 + 4)] += w2[(size_t)(o * IC + i)];  // [oc][ic][kh][kw]
+        b1[(size_t)o] += b2[(size_t)o];
+    }
+    std::vector<float> wr((size_t)(9 * IC * OC)), wg4((size_t)(36 * IC * OC));
+    if (ppdl_hip_repack_conv(w.data(), OC, IC, 3, wr.data(), wg4.data()) != PPDL_OK) {
+        *err = "repack failed: " + bp + ".rep";
+        return false;
+    }
+    w_[bp + ".rep.wr"] = upload(wr);
+    w_[bp + ".rep.wg4"] = upload(wg4);
+    w_[bp + ".rep.bias"] = upload(b1);
+    ne_[bp + ".rep.weight"] = t1.ne;
     return true;
 }
 
@@ -638,11 +678,18 @@ void Net::hg_block(const Img &cat, int cin, const std::string &pfx, bool light, 
 // csp (:662-668): a = c1(x); 3x repvgg; b = c2(x); a + b.  repvgg (:656-660)
 // = silu(c1_3x3(a) + c2_1x1(a)); the sums ride in the 1x1 convs' epilogues.
 Img Net::csp(const Img &x, const std::string &pfx, float *out) {
+    // PPDL_REPVGG=0 keeps the two-conv form of the RepVGG blocks (A/B runs)
+    const char *e = getenv("PPDL_REPVGG");
+    const bool fold = !(e && e[0] == '0');
     Img a = conv(x, pfx + ".c1", 1, 0, kActSilu);
     for (int i = 0; i < 3; i++) {
         const std::string bp = pfx + ".bn" + std::to_string(i);
-        Img t = conv(a, bp + ".c1", 1, 1, kActNone);
-        a = conv(a, bp + ".c2", 1, 0, kActSilu, nullptr, 0, t.d, 1);
+        if (fold && w_.count(bp + ".rep.wg4")) {
+            a = conv(a, bp + ".rep", 1, 1, kActSilu);  // silu(3x3 with the 1x1 folded into its centre tap)
+        } else {
+            Img t = conv(a, bp + ".c1", 1, 1, kActNone);
+            a = conv(a, bp + ".c2", 1, 0, kActSilu, nullptr, 0, t.d, 1);
+        }
     }
     return conv(x, pfx + ".c2", 1, 0, kActSilu, out, 0, a.d, 2);
 }
