@@ -28,6 +28,16 @@ extern "C" {
 
 #define PPDL_MAGIC 0x5050444C /* "PPDL", op_params[12] */
 
+/* F(4,3) matrix-set tag, op_params[11] of ops 10, 11, 12, 15 and 17 (an
+ * extension: the reference leaves slot 11 zero).  These ops use this
+ * library's own Winograd matrices (ppdl_hip_wg4_matrices), so their .wg4
+ * weights must come from ppdl_hip_repack_conv; the reference's host repack
+ * (src/ppdoclayout.cpp:313-337) builds .wg4 with other matrices, and
+ * mixing the two gives wrong convolutions without any error.  A host sets
+ * this tag where it switches its repack to ppdl_hip_repack_conv; without it
+ * the ops return PPDL_EINVAL. */
+#define PPDL_WG4_SET 0x57473433 /* "WG43" */
+
 /* Op ids (op_params[13]).  Ids 1..13 keep the reference's numbering and
  * parameter encoding (patches/ggml-ppdl.patch:120-132); ids >= 14 are fused
  * extensions emitted only by this project's own host. */

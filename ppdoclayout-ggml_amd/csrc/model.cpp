@@ -114,6 +114,7 @@ ppdl_tview row_view(const float *d, int64_t cols, int64_t rows, int64_t ld) {
 
 std::vector<int32_t> op_params(int op, int p14, int p15) {
     std::vector<int32_t> v(16, 0);
+    v[11] = (int32_t)PPDL_WG4_SET;  // every .wg4 here comes from ppdl_hip_repack_conv
     v[12] = (int32_t)PPDL_MAGIC;
     v[13] = op;
     v[14] = p14;

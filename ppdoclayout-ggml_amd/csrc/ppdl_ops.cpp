@@ -133,6 +133,15 @@ int check_conv1x1(const int32_t *p, const ppdl_tview *dst, const ppdl_tview *src
 }
 
 int check_op(const int32_t *p, const ppdl_tview *dst, const ppdl_tview *src, int nsrc) {
+    switch (p[13]) {
+        case PPDL_OP_WG4_INPUT: case PPDL_OP_WG4_OUTPUT: case PPDL_OP_WG4_MADD: case PPDL_OP_WG4_INPUT_PAD:
+        case PPDL_OP_WG4_CONV:
+            // .wg4 made with another F(4,3) matrix set would pass every shape check
+            if ((uint32_t)p[11] != (uint32_t)PPDL_WG4_SET) return PPDL_EINVAL;
+            break;
+        default:
+            break;
+    }
     const int wi = ws_index(p);
     if (wi >= 0 && nsrc > wi && !ws_valid(&src[wi])) return PPDL_EINVAL;
     switch (p[13]) {

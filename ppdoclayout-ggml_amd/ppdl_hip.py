@@ -14,6 +14,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "lib", "libppdl_hip.so")
 
 PPDL_MAGIC = 0x5050444C
+WG4_SET = 0x57473433  # op_params[11] of the F(4,3) ops: .wg4 from this library's repack
 
 OP_MASKBOX = 1
 OP_MSDEF = 2
@@ -105,9 +106,13 @@ def lib():
     return _lib
 
 
-def params(op, p14=0, p15=0):
-    """op_params[16] with the tag in slots 12/13 (src/ppdoclayout.cpp:48-53)."""
+def params(op, p14=0, p15=0, wg4_set=True):
+    """op_params[16] with the tag in slots 12/13 (src/ppdoclayout.cpp:48-53)
+    and, unless wg4_set is False, the F(4,3) matrix-set tag in slot 11 (this
+    binding's .wg4 weights come from repack_conv)."""
     p = (ctypes.c_int32 * 16)()
+    if wg4_set:
+        p[11] = ctypes.c_int32(WG4_SET).value
     p[12] = ctypes.c_int32(PPDL_MAGIC).value
     p[13] = op
     p[14] = ctypes.c_int32(p14).value

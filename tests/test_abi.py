@@ -105,6 +105,30 @@ def test_run_rejects_bad_nodes_without_launching(hip):
     assert hip.run(hip.OP_BIASACT, hip.raw_view(0, [4]), [v([4]), v([1])], stream=0) == hip.EINVAL
 
 
+def test_wg4_ops_require_the_matrix_set_tag(hip):
+    """Ops 10/11/12/15/17 return EINVAL unless op_params[11] carries
+    PPDL_WG4_SET (the caller's .wg4 came from this library's repack); the
+    other ops ignore slot 11."""
+    import ctypes
+    v = lambda ne: hip.raw_view(FAKE, ne)  # noqa: E731
+    cases = [
+        (hip.OP_WG4_INPUT, v([25, 16, 36]), [v([22, 22, 16])], 25, 5),
+        (hip.OP_WG4_INPUT_PAD, v([25, 16, 36]), [v([20, 20, 16])], 25, 5),
+        (hip.OP_WG4_MADD, v([25, 8, 36]), [v([25, 16, 36]), v([8, 16, 36])], 0, 0),
+        (hip.OP_WG4_OUTPUT, v([20, 20, 8]), [v([25, 8, 36]), v([8])], 0, 5),
+        (hip.OP_WG4_CONV, v([20, 20, 16]), [v([20, 20, 8]), v([16, 8, 36]), v([16])], 1, 0),
+    ]
+    L = hip.lib()
+    for op, d, srcs, p14, p15 in cases:
+        dd, arr, n = hip._views(d, srcs)
+        assert L.ppdl_hip_supports(hip.params(op, p14, p15), ctypes.byref(dd), arr, n) == 1, op
+        assert L.ppdl_hip_supports(hip.params(op, p14, p15, wg4_set=False), ctypes.byref(dd), arr, n) == 0, op
+        assert L.ppdl_hip_run(hip.params(op, p14, p15, wg4_set=False), ctypes.byref(dd), arr, n, None) == hip.EINVAL
+    # a non-Winograd op is indifferent to the tag
+    dd, arr, n = hip._views(v([10, 10, 8]), [v([10, 10, 16]), v([8, 16, 1]), v([8])])
+    assert L.ppdl_hip_supports(hip.params(hip.OP_CONV1X1_BA, 1, 0, wg4_set=False), ctypes.byref(dd), arr, n) == 1
+
+
 def test_supports_with_views_uses_the_same_validation(hip):
     v = lambda ne: hip.raw_view(FAKE, ne)  # noqa: E731
     good = (v([10, 10, 8]), [v([10, 10, 16]), v([8, 16, 1]), v([8])])
