@@ -122,35 +122,10 @@ __device__ __forceinline__ float invsig(float x) {
     return logf(x1 / x2);
 }
 
-__global__ __launch_bounds__(256) void k_mask_box(const float *__restrict__ ml,
-                                                  float *__restrict__ out, int nq) {
-    const int q = blockIdx.x;
-    if (q >= nq) return;
-    const float4 *m4 = reinterpret_cast<const float4 *>(ml + (int64_t)q * kMaskPix);
-    int xmin = kMaskHW, xmax = -1, ymin = kMaskHW, ymax = -1;
-    // 8 float4 loads in flight per thread and step (indices past the mask
-    // clamped, their values ignored); branch-free integer min / max, exact
-    // in any order
-    constexpr int kN4 = kMaskPix / 4, kU = 8;
-    for (int i0 = threadIdx.x; i0 < kN4; i0 += 256 * kU) {
-        float4 v[kU];
-#pragma unroll
-        for (int u = 0; u < kU; u++) v[u] = m4[min(i0 + u * 256, kN4 - 1)];
-#pragma unroll
-        for (int u = 0; u < kU; u++) {
-            const int i = i0 + u * 256;
-            const int y = (4 * i) / kMaskHW, x = 4 * i - y * kMaskHW;  // 200 % 4 == 0: same row
-            const float e[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const bool pos = i < kN4 && e[j] > 0.0f;
-                xmin = min(xmin, pos ? x + j : kMaskHW);
-                xmax = max(xmax, pos ? x + j : -1);
-                ymin = min(ymin, pos ? y : kMaskHW);
-                ymax = max(ymax, pos ? y : -1);
-            }
-        }
-    }
+// the box of the block's (xmin, xmax, ymin, ymax) after the per-thread
+// partials: wave shuffles, then wave 0's thread 0 over the 4 waves, then the
+// inverse-sigmoid cxcywh normalised by 200 ((0, 0, 0, 0) for an empty mask)
+__device__ __forceinline__ void box_finish(int xmin, int xmax, int ymin, int ymax, float *o) {
 #pragma unroll
     for (int s = 32; s > 0; s >>= 1) {
         xmin = min(xmin, __shfl_xor(xmin, s));
@@ -189,12 +164,78 @@ __global__ __launch_bounds__(256) void k_mask_box(const float *__restrict__ ml,
         by1 /= (float)kMaskHW;
         const float cx = (bx0 + bx1) * 0.5f, cy = (by0 + by1) * 0.5f;
         const float bw = bx1 - bx0, bh = by1 - by0;
-        float *o = out + (int64_t)q * 4;
         o[0] = invsig(cx);
         o[1] = invsig(cy);
         o[2] = invsig(bw);
         o[3] = invsig(bh);
     }
+}
+
+__global__ __launch_bounds__(256) void k_mask_box(const float *__restrict__ ml,
+                                                  float *__restrict__ out, int nq) {
+    const int q = blockIdx.x;
+    if (q >= nq) return;
+    const float4 *m4 = reinterpret_cast<const float4 *>(ml + (int64_t)q * kMaskPix);
+    int xmin = kMaskHW, xmax = -1, ymin = kMaskHW, ymax = -1;
+    // 8 float4 loads in flight per thread and step (indices past the mask
+    // clamped, their values ignored); branch-free integer min / max, exact
+    // in any order
+    constexpr int kN4 = kMaskPix / 4, kU = 8;
+    for (int i0 = threadIdx.x; i0 < kN4; i0 += 256 * kU) {
+        float4 v[kU];
+#pragma unroll
+        for (int u = 0; u < kU; u++) v[u] = m4[min(i0 + u * 256, kN4 - 1)];
+#pragma unroll
+        for (int u = 0; u < kU; u++) {
+            const int i = i0 + u * 256;
+            const int y = (4 * i) / kMaskHW, x = 4 * i - y * kMaskHW;  // 200 % 4 == 0: same row
+            const float e[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const bool pos = i < kN4 && e[j] > 0.0f;
+                xmin = min(xmin, pos ? x + j : kMaskHW);
+                xmax = max(xmax, pos ? x + j : -1);
+                ymin = min(ymin, pos ? y : kMaskHW);
+                ymax = max(ymax, pos ? y : -1);
+            }
+        }
+    }
+    box_finish(xmin, xmax, ymin, ymax, out + (int64_t)q * 4);
+}
+
+// mask -> box from sign bits: each thread takes words of 32 pixels; a word
+// covers at most two rows of 200 (bits below `cut` on row y0, the rest on
+// y0 + 1), and the first / last set bit of each part give its extreme
+// columns.  Same min / max and the same finish as k_mask_box.
+__global__ __launch_bounds__(256) void k_mask_box_bits(const uint32_t *__restrict__ bits, float *__restrict__ out,
+                                                       int nq) {
+    const int q = blockIdx.x;
+    if (q >= nq) return;
+    constexpr int kW = kMaskPix / 32;
+    const uint32_t *bq = bits + (int64_t)q * kW;
+    int xmin = kMaskHW, xmax = -1, ymin = kMaskHW, ymax = -1;
+    for (int w = threadIdx.x; w < kW; w += 256) {
+        const uint32_t v = bq[w];
+        const int p0 = 32 * w, y0 = p0 / kMaskHW;
+        const int cut = kMaskHW * (y0 + 1) - p0;  // >= 1
+        const uint32_t lo = cut >= 32 ? v : (v & ((1u << cut) - 1u));
+        const uint32_t hi = cut >= 32 ? 0u : (v & ~((1u << cut) - 1u));
+        if (lo) {
+            const int xb = p0 - kMaskHW * y0;
+            xmin = min(xmin, xb + __builtin_ctz(lo));
+            xmax = max(xmax, xb + 31 - __builtin_clz(lo));
+            ymin = min(ymin, y0);
+            ymax = max(ymax, y0);
+        }
+        if (hi) {
+            const int xb = p0 - kMaskHW * (y0 + 1);
+            xmin = min(xmin, xb + __builtin_ctz(hi));
+            xmax = max(xmax, xb + 31 - __builtin_clz(hi));
+            ymin = min(ymin, y0 + 1);
+            ymax = max(ymax, y0 + 1);
+        }
+    }
+    box_finish(xmin, xmax, ymin, ymax, out + (int64_t)q * 4);
 }
 
 // ---------------------------------------------------------------------------
@@ -343,6 +384,11 @@ hipError_t msdeform(const float *val, int ldv, const float *off, int ldo, const 
 
 hipError_t mask_box(const float *ml, float *out, int nq, hipStream_t s) {
     hipLaunchKernelGGL(k_mask_box, dim3(nq), dim3(256), 0, s, ml, out, nq);
+    return hipGetLastError();
+}
+
+hipError_t mask_box_bits(const uint32_t *bits, float *out, int nq, hipStream_t s) {
+    hipLaunchKernelGGL(k_mask_box_bits, dim3(nq), dim3(256), 0, s, bits, out, nq);
     return hipGetLastError();
 }
 

@@ -133,6 +133,27 @@ __device__ __forceinline__ void gemm_epilogue(const f32x16 (&acc)[TM][TN], const
         return;
     }
 
+    if (g.bits) {
+        // sign bits of the products: a half-wave holds 32 consecutive n of one
+        // row (the launch checks N % 32 == 0), so one ballot per register
+        // yields row m's word (lanes 0-31) and row m + 4's (lanes 32-63)
+        const int nwords = N >> 5;
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+            const int n0 = nw + j * 32;
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int r = RB; r < RB + RN; r++) {
+                    const unsigned long long b = __ballot(acc[i][j][r] > 0.0f);
+                    const int m = mw + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                    if ((lane & 31) == 0 && m < M && n0 < N)
+                        g.bits[(int64_t)bz * M * nwords + (int64_t)m * nwords + (n0 >> 5)] =
+                            (uint32_t)(lane ? (b >> 32) : b);
+                }
+        }
+        return;
+    }
     const float *__restrict__ bias = g.bias;
     const int act = g.act, add_mode = g.add_mode, bias_n = g.bias_n;
     float *__restrict__ C = g.C + (int64_t)bz * g.sC;
@@ -1645,6 +1666,9 @@ hipError_t dispatch(const GemmArgs &g_in, const GemmWorkspace &ws, hipStream_t s
     }
     const GemmPlan p = gemm_plan(g, ws.bytes, BMODE == 1);
     if (g.a_add && (BMODE != 0 || !g.a_rowmajor || (((uintptr_t)g.a_add) & 15) != 0 || g.a_add_n % 32 != 0))
+        return hipErrorInvalidValue;
+    // sign-bit output: the tiled kernels' shared epilogue, whole 32-column words
+    if (g.bits && (p.cfg == kCfgSmall || p.splits > 1 || g.c_trans || g.N % 32 != 0 || g.a_w4 || BMODE != 0))
         return hipErrorInvalidValue;
     if (BMODE == 0 && p.cfg == kCfgSmall) {
         if (g.a_rowmajor && (g.K % 4 != 0 || g.lda % 4 != 0 || (((uintptr_t)g.A) & 15) != 0))

@@ -149,6 +149,7 @@ class Net {
     // the host result's inputs: mask sign bits packed on the device, then
     // logits, boxes, order and the bits copied into pinned buffers
     bool download(float *logits, float *boxes, float *order, uint32_t *mbits);
+    bool mask_logits();  // masks_ = the final mask logits of the last replay
 
     int nodes() const {
         int k = 0;
@@ -159,7 +160,8 @@ class Net {
     // outputs
     float *logits_ = nullptr, *boxes_ = nullptr, *order_ = nullptr, *masks_ = nullptr, *refu_ = nullptr;
     int32_t *topk_ = nullptr;
-    uint32_t *mbits_ = nullptr;  // sign bits of masks_, packed after a replay for the host result
+    uint32_t *mbits_ = nullptr;  // sign bits of the final mask logits, written by the graph
+    GemmArgs mask_logits_{};     // the final mask logits into masks_ (run on request, not in the graph)
     std::vector<DumpRec> dumps_;
 
    private:
@@ -242,7 +244,7 @@ class Net {
         n.flops = 2.0 * g.M * (double)g.N * g.K * g.batch;
         // the implicit-im2col B is the input image, read once
         const double b_elems = im2col ? (double)g.IC * g.IH * g.IW : (double)g.K * g.N;
-        n.bytes = 4.0 * g.batch * ((double)g.M * g.K + b_elems + (double)g.M * g.N);
+        n.bytes = 4.0 * g.batch * ((double)g.M * g.K + b_elems + (g.bits ? g.M * (double)g.N / 32.0 : (double)g.M * g.N));
         n.kern = gemm_kernel_name(g, ws_bytes, im2col);
     }
     // one tagged op through the C-ABI; a GEMM op gets the shared split-K
@@ -850,7 +852,12 @@ bool Net::build(bool dumps, std::string *err) {
     dump("target", target.d, {kDM, NQ});
 
     // enhanced reference from the encoder masks (:808-822)
-    auto masks_of = [&](const Seq &mq, float *out, const char *nm) {
+    // mask logits = mask queries x prototypes.  Inference only needs their
+    // signs (the box of each encoder mask, the final binary masks), so the
+    // graph's GEMMs store sign bits from the epilogue (1.5 MB instead of
+    // 48 MB each); the logits themselves are computed in dump mode and on
+    // request (ppdl_get_raw) by the same GEMM without the bits.
+    auto masks_args = [&](const Seq &mq, float *out, uint32_t *bits) {
         GemmArgs g{};
         g.A = mq.d;
         g.lda = mq.ld;
@@ -863,16 +870,21 @@ bool Net::build(bool dumps, std::string *err) {
         g.N = NPIX;
         g.K = 32;
         g.batch = 1;
-        gemm(nm, g);
+        g.bits = bits;
+        return g;
     };
     Seq outq0 = ln(target, nullptr, "dec_norm");
     Seq mq0 = mlp3(outq0, "mq");
-    float *encm = alloc((int64_t)NQ * NPIX);
+    uint32_t *encbits = (uint32_t *)alloc((int64_t)NQ * (NPIX / 32));
     join(1);
-    masks_of(mq0, encm, "enc_masks");
-    dump("enc_masks", encm, {NPIX, NQ});
+    gemm("enc_masks", masks_args(mq0, nullptr, encbits));
+    if (want_dumps_) {
+        float *encm = alloc((int64_t)NQ * NPIX);
+        gemm("enc_masks.logits", masks_args(mq0, encm, nullptr));
+        dump("enc_masks", encm, {NPIX, NQ});
+    }
     refu_ = alloc((int64_t)NQ * 4);
-    tagged("mask_box", PPDL_OP_MASKBOX, 0, 0, view(refu_, {4, NQ}), {view(encm, {NPIX, NQ})});
+    node("mask_box", 1, [=](hipStream_t st) { return ok(mask_box_bits(encbits, refu_, NQ, st)); });
     dump("init_ref_unact", refu_, {4, NQ});
     boxes_ = alloc((int64_t)NQ * 4);
     node("ref0", 1, [=](hipStream_t st) {
@@ -913,8 +925,9 @@ bool Net::build(bool dumps, std::string *err) {
     logits_ = lg.d;
     Seq mq6 = mlp3(outq, "mq");
     masks_ = alloc((int64_t)NQ * NPIX);
-    masks_of(mq6, masks_, "masks");
     mbits_ = (uint32_t *)alloc((int64_t)NQ * (NPIX / 32));
+    gemm("masks", masks_args(mq6, nullptr, mbits_));  // the result's binary masks
+    mask_logits_ = masks_args(mq6, masks_, nullptr);
     Seq gp = lin(lin(xq, "order5", kActNone), "gp", kActNone);  // (300, 128)
     order_ = alloc((int64_t)NQ * NQ);
     node("order", 1, [=](hipStream_t st) { return ok(order_logits(gp.d, order_, NQ, 64, 1.0f / 8.0f, st)); });
@@ -1042,12 +1055,16 @@ bool Net::upload_image(const float *host) {
 
 bool Net::download(float *logits, float *boxes, float *order, uint32_t *mbits) {
     const hipStream_t s = stream_;
-    return mask_bits(masks_, mbits_, NQ, NPIX, s) == hipSuccess &&
-           hipMemcpyAsync(logits, logits_, (size_t)NQ * NC * 4, hipMemcpyDeviceToHost, s) == hipSuccess &&
+    return hipMemcpyAsync(logits, logits_, (size_t)NQ * NC * 4, hipMemcpyDeviceToHost, s) == hipSuccess &&
            hipMemcpyAsync(boxes, boxes_, (size_t)NQ * 4 * 4, hipMemcpyDeviceToHost, s) == hipSuccess &&
            hipMemcpyAsync(order, order_, (size_t)NQ * NQ * 4, hipMemcpyDeviceToHost, s) == hipSuccess &&
            hipMemcpyAsync(mbits, mbits_, (size_t)NQ * (NPIX / 32) * 4, hipMemcpyDeviceToHost, s) == hipSuccess &&
            hipStreamSynchronize(s) == hipSuccess;
+}
+
+bool Net::mask_logits() {
+    return gemm_dense(mask_logits_, GemmWorkspace{nullptr, 0}, stream_) == hipSuccess &&
+           hipStreamSynchronize(stream_) == hipSuccess;
 }
 
 int Net::replay() {
@@ -1121,8 +1138,8 @@ int Net::profile_nodes(int iters, ppdl_node_stat *out, int cap) {
 
 // ---------------------------------------------------------------------------
 // Host result assembly: the reference's postprocess (src/ppdoclayout.cpp:
-// 927-993) on this runtime's downloads.  The device has packed the mask
-// logits into sign bits (mask_bits), so 1.5 MB crosses PCIe instead of 48 MB.
+// 927-993) on this runtime's downloads.  The graph's mask GEMM stores the
+// logits' sign bits, so 1.5 MB crosses PCIe instead of 48 MB.
 // On the host:
 //   * every (query, class) logit is scored with the logistic function, and
 //     the 300 best are picked by a 64-bit key: the score's order-preserving
@@ -1401,7 +1418,13 @@ extern "C" PPDL_API int64_t ppdl_get_raw(ppdl_ctx *c, int which, void *dst, int6
         case 0: src = c->net->logits_; cnt = (int64_t)NQ * NC; break;
         case 1: src = c->net->boxes_; cnt = (int64_t)NQ * 4; break;
         case 2: src = c->net->order_; cnt = (int64_t)NQ * NQ; break;
-        case 3: src = c->net->masks_; cnt = (int64_t)NQ * NPIX; break;
+        case 3:
+            // the final mask logits: the graph keeps only their signs, so the
+            // same GEMM runs once more without the bits, on the graph's inputs
+            if (!c->net->mask_logits()) return -1;
+            src = c->net->masks_;
+            cnt = (int64_t)NQ * NPIX;
+            break;
         case 4: src = c->net->topk_; cnt = NQ; break;
         case 5: src = c->net->refu_; cnt = (int64_t)NQ * 4; break;
         default: return -1;

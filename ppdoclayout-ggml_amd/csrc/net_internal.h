@@ -27,8 +27,6 @@ hipError_t mul_rows(const float *x, const float *mask, float *out, int64_t T, in
 hipError_t box_update(const float *delta, float *ref, int n, hipStream_t s);
 hipError_t get_rows(const float *src, const int32_t *idx, float *out, int nrows, hipStream_t s);
 hipError_t order_logits(const float *gp, float *out, int nq, int hd, float scale, hipStream_t s);
-// bits[q][w] bit b = (ml[q][32w + b] > 0), npix % 32 == 0, 16-byte aligned ml
-hipError_t mask_bits(const float *ml, uint32_t *bits, int nq, int npix, hipStream_t s);
 // in [rows][cols] -> out[c][r] with row stride ldo
 hipError_t transpose(const float *in, float *out, int rows, int cols, int ldo, hipStream_t s);
 

@@ -415,38 +415,9 @@ __global__ __launch_bounds__(256) void k_transpose(const float *__restrict__ in,
         if (c0 + c < cols && r0 + tx < rows) out[(int64_t)(c0 + c) * ldo + r0 + tx] = tile[tx][c];
 }
 
-// Mask binarisation for the host result (src/ppdoclayout.cpp:985 keeps
-// logit > 0 per pixel): bit b of word w of row q is pixel 32w + b of query q.
-// One thread packs one word from eight float4 loads (npix % 32 == 0, 16-byte
-// aligned rows: checked on the host), so the host downloads 1/32 of the
-// logits' bytes.
-__global__ __launch_bounds__(256) void k_mask_bits(const float *__restrict__ ml, uint32_t *__restrict__ bits,
-                                                   int64_t nwords) {
-    const int64_t w = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (w >= nwords) return;
-    const float4 *src = reinterpret_cast<const float4 *>(ml) + w * 8;
-    uint32_t word = 0;
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-        const float4 v = src[i];
-        word |= (v.x > 0.0f ? 1u : 0u) << (4 * i + 0);
-        word |= (v.y > 0.0f ? 1u : 0u) << (4 * i + 1);
-        word |= (v.z > 0.0f ? 1u : 0u) << (4 * i + 2);
-        word |= (v.w > 0.0f ? 1u : 0u) << (4 * i + 3);
-    }
-    bits[w] = word;
-}
-
 unsigned blocks_for(int64_t n) { return (unsigned)((n + 255) / 256); }
 
 }  // namespace
-
-hipError_t mask_bits(const float *ml, uint32_t *bits, int nq, int npix, hipStream_t s) {
-    if (nq < 1 || npix < 32 || npix % 32 != 0 || (((uintptr_t)ml) & 15) != 0) return hipErrorInvalidValue;
-    const int64_t nwords = (int64_t)nq * (npix / 32);
-    hipLaunchKernelGGL(k_mask_bits, dim3(blocks_for(nwords)), dim3(256), 0, s, ml, bits, nwords);
-    return hipGetLastError();
-}
 
 hipError_t dwconv(const float *x, const float *w, const float *b, float *out, int C, int IH, int IW, int K, int S,
                   int P, int act, int64_t in_plane, int64_t out_plane, hipStream_t s) {

@@ -85,6 +85,10 @@ struct GemmArgs {
     // into the GEMM that consumes it.
     const float *a_w4;
     const float *a_b4;
+    // Sign-bit output (k_gemm / k_gemm_dma epilogues, no split-K, N % 32 ==
+    // 0): with bits set the results are not stored; bit n % 32 of word
+    // bits[m * (N / 32) + n / 32] is (acc > 0), before any bias or act.
+    uint32_t *bits;
 };
 
 // act codes of the GEMM epilogue and the elementwise kernels
@@ -146,6 +150,9 @@ hipError_t im2col_ggml(const float *x, float *dst, int64_t IW, int64_t IH, int64
 hipError_t msdeform(const float *val, int ldv, const float *off, int ldo, const float *awr, int ldw,
                     const float *ref, float *out, int nq, hipStream_t s);
 hipError_t mask_box(const float *ml, float *out, int nq, hipStream_t s);
+// the same boxes from the masks' sign bits [nq][40000 / 32] (bit p % 32 of
+// word p / 32: logit of pixel p > 0), bit-identical to mask_box
+hipError_t mask_box_bits(const uint32_t *bits, float *out, int nq, hipStream_t s);
 // ws (optional, >= 8 * ntok bytes): per-token keys, computed grid-wide first
 hipError_t topk(const float *logits, int32_t *out, int ntok, int nc, int nq, void *ws, int64_t ws_bytes,
                 hipStream_t s);
