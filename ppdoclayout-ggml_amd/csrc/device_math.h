@@ -35,6 +35,21 @@ __device__ __forceinline__ int xcd_remap(int hw, int n) {
     return xcd * q + (xcd < r ? xcd : r) + slot;
 }
 
+// Sum over the 64 lanes of a wave, the same value in every lane: DPP steps
+// inside each row of 16 lanes (quad swaps, then half-row and row mirrors),
+// then the four row totals read out and added in lane order.  Every step
+// pairs equal partial sums, so all lanes hold bit-identical results.
+__device__ __forceinline__ float wave_sum(float x) {
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0xB1, 0xF, 0xF, false));   // [1,0,3,2]
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x4E, 0xF, 0xF, false));   // [2,3,0,1]
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x141, 0xF, 0xF, false));  // half mirror
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x140, 0xF, 0xF, false));  // row mirror
+    const int xi = __float_as_int(x);
+    return ((__int_as_float(__builtin_amdgcn_readlane(xi, 0)) + __int_as_float(__builtin_amdgcn_readlane(xi, 16))) +
+            __int_as_float(__builtin_amdgcn_readlane(xi, 32))) +
+           __int_as_float(__builtin_amdgcn_readlane(xi, 48));
+}
+
 // box refinement (src/ppdoclayout.cpp:860-862): sigmoid(delta + inv_sigmoid(ref))
 __device__ __forceinline__ float refine_box(float delta, float ref) {
     return 1.0f / (1.0f + expf(-(delta + inv_sigmoid(ref))));

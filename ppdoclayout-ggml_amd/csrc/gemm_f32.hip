@@ -1348,6 +1348,26 @@ __global__ __launch_bounds__(WV * 64) void k_gemm_small(GemmArgs g, int tiles_m,
         }
     };
 
+    // the epilogue's bias and residual operands, fetched now so that their
+    // latency overlaps the operand loads (clamped indices: always in range).
+    // Only with 8 or 16 waves: with 4, the 8 extra registers cost a wave
+    // per SIMD (measured 0.35 us slower per launch on the 1x1 convs).
+    const float *__restrict__ bias = g.bias;
+    float *__restrict__ C = g.C + (int64_t)bz * g.sC;
+    const float *__restrict__ Ad = g.add ? g.add + (int64_t)bz * g.sC : nullptr;
+    constexpr int EP = 1024 / NT;
+    constexpr bool PF = WV >= 8;
+    float eb[EP], ea[EP];
+#pragma unroll
+    for (int i = 0; i < EP && PF; i++) {
+        const int fast = tid & 31, slow = (tid >> 5) + (NT / 32) * i;
+        const int mm = g.c_trans ? fast : slow, nn = g.c_trans ? slow : fast;
+        const int m = min(m0 + mm, M - 1), n = min(n0 + nn, N - 1);
+        const int64_t idx = g.c_trans ? (int64_t)n * g.ldc + m : (int64_t)m * g.ldc + n;
+        eb[i] = bias ? bias[g.bias_n ? n : m] : 0.0f;
+        ea[i] = g.add_mode && Ad ? Ad[idx] : 0.0f;
+    }
+
     f32x16 acc;
 #pragma unroll
     for (int r = 0; r < 16; r++) acc[r] = 0.0f;
@@ -1378,12 +1398,9 @@ __global__ __launch_bounds__(WV * 64) void k_gemm_small(GemmArgs g, int tiles_m,
     for (int r = 0; r < 16; r++) red[wave][8 * (r >> 2) + 4 * h + (r & 3)][l32] = acc[r];
     __syncthreads();
 
-    const float *__restrict__ bias = g.bias;
-    float *__restrict__ C = g.C + (int64_t)bz * g.sC;
-    const float *__restrict__ Ad = g.add ? g.add + (int64_t)bz * g.sC : nullptr;
     // NT threads x 1024/NT outputs; consecutive threads along the contiguous axis of C
 #pragma unroll
-    for (int i = 0; i < 1024 / NT; i++) {
+    for (int i = 0; i < EP; i++) {
         const int fast = tid & 31, slow = (tid >> 5) + (NT / 32) * i;
         const int mm = g.c_trans ? fast : slow, nn = g.c_trans ? slow : fast;
         const int m = m0 + mm, n = n0 + nn;
@@ -1392,11 +1409,13 @@ __global__ __launch_bounds__(WV * 64) void k_gemm_small(GemmArgs g, int tiles_m,
 #pragma unroll
             for (int w = 1; w < WV; w++) v += red[w][mm][nn];
             const int64_t idx = g.c_trans ? (int64_t)n * g.ldc + m : (int64_t)m * g.ldc + n;
-            if (bias) v += bias[g.bias_n ? n : m];
-            if (g.add_mode == 1) v += Ad[idx];
+            const float bv = PF ? eb[i] : (bias ? bias[g.bias_n ? n : m] : 0.0f);
+            const float av = PF ? ea[i] : (g.add_mode ? Ad[idx] : 0.0f);
+            if (bias) v += bv;
+            if (g.add_mode == 1) v += av;
             v = act_f(v, g.act);
-            if (g.add_mode == 2) v += Ad[idx];
-            else if (g.add_mode == 3) v = refine_box(v, Ad[idx]);
+            if (g.add_mode == 2) v += av;
+            else if (g.add_mode == 3) v = refine_box(v, av);
             C[idx] = v;
         }
     }
@@ -1647,6 +1666,19 @@ hipError_t launch_small(const GemmArgs &g, hipStream_t s) {
     return launch_small_wv<AMODE, false>(g, wv, grid, tiles_m, tmn, s);
 }
 
+// Where the 16x16-MFMA tile menu (gemm_lt.hip) replaces the plan: single
+// 1x1 convs on maps of at most 4096 pixels that the plan would split along K
+// with K <= 1536 (one pass instead of split partials plus a reduction
+// launch).  In-graph kernel traces on the network: enc_in1 44 -> 28 us,
+// stage-3 agg1 62 -> 46 us, the 1024-channel stage-2 l0 1x1s 22 -> 20 us.
+// Where it lost in the graph: the 4-wave small-kernel shapes (8.0 -> 8.7 us;
+// faster only in isolated back-to-back replays), the batched F(4,3) planes,
+// the 25x25 shapes of the 16-wave small kernel, the unsplit 64x64 GEMMs and
+// the long-K (>= 1664) split aggregations.
+bool lt_wanted(const GemmArgs &g, const GemmPlan &p) {
+    return g.batch == 1 && g.N <= 4096 && p.cfg != kCfgSmall && p.splits > 1 && g.K <= 1536;
+}
+
 template <int BMODE>
 hipError_t dispatch(const GemmArgs &g_in, const GemmWorkspace &ws, hipStream_t s) {
     GemmArgs g = g_in;
@@ -1665,6 +1697,10 @@ hipError_t dispatch(const GemmArgs &g_in, const GemmWorkspace &ws, hipStream_t s
         return launch_small<2>(g, s);
     }
     const GemmPlan p = gemm_plan(g, ws.bytes, BMODE == 1);
+    if constexpr (BMODE == 0) {
+        const int lc = gemm_lt_pick(g, 8 * cus_per_xcd(), lt_wanted(g, p));
+        if (lc >= 0) return gemm_lt(g, lc, s);
+    }
     if (g.a_add && (BMODE != 0 || !g.a_rowmajor || (((uintptr_t)g.a_add) & 15) != 0 || g.a_add_n % 32 != 0))
         return hipErrorInvalidValue;
     // sign-bit output: the tiled kernels' shared epilogue, whole 32-column words
@@ -1743,6 +1779,12 @@ std::string gemm_kernel_name(const GemmArgs &g, int64_t ws_bytes, bool im2col) {
     if (im2col && frag_ok(g)) return "k_conv_frag<" + std::to_string(frag_waves(g)) + ">";
     if (g.a_w4) return "k_gemm_small<2, " + std::to_string(small_waves(g.K, small_tiles(g))) + ", false>";
     const GemmPlan p = gemm_plan(g, ws_bytes, im2col);
+    if (!im2col) {
+        GemmArgs gv = g;
+        gv.n_vec = n_vec_of(g);
+        const int lc = gemm_lt_pick(gv, 8 * cus_per_xcd(), lt_wanted(gv, p));
+        if (lc >= 0) return gemm_lt_name(lc);
+    }
     if (p.cfg == kCfgSmall)
         return std::string("k_gemm_small<") + (g.a_rowmajor ? "1, " : "0, ") +
                std::to_string(small_waves(g.K, small_tiles(g))) + (g.a_add && g.a_rowmajor ? ", true>" : ", false>");

@@ -183,29 +183,27 @@ __global__ __launch_bounds__(256) void k_layernorm(const float *__restrict__ a, 
     const int lane = threadIdx.x & 63;
     if (t >= T) return;
     const float4 av = *reinterpret_cast<const float4 *>(a + (int64_t)t * kDM + lane * 4);
+    // without b the second row load re-reads a (selected address, no branch
+    // between the loads) and is not added
+    const float4 bv0 = *reinterpret_cast<const float4 *>((b ? b : a) + (int64_t)t * kDM + lane * 4);
+    const float4 gv = *reinterpret_cast<const float4 *>(gamma + lane * 4);
+    const float4 bv = *reinterpret_cast<const float4 *>(beta + lane * 4);
+    __builtin_amdgcn_sched_barrier(0);  // all four loads in flight before the reductions
     float v[4] = {av.x, av.y, av.z, av.w};
     if (b) {
-        const float4 bv = *reinterpret_cast<const float4 *>(b + (int64_t)t * kDM + lane * 4);
-        v[0] += bv.x;
-        v[1] += bv.y;
-        v[2] += bv.z;
-        v[3] += bv.w;
+        v[0] += bv0.x;
+        v[1] += bv0.y;
+        v[2] += bv0.z;
+        v[3] += bv0.w;
     }
-    float s = (v[0] + v[1]) + (v[2] + v[3]);
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
-    const float mean = s / (float)kDM;
+    const float mean = wave_sum((v[0] + v[1]) + (v[2] + v[3])) / (float)kDM;
     float q = 0.0f;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         v[i] -= mean;
         q += v[i] * v[i];
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) q += __shfl_xor(q, o);
-    const float scale = 1.0f / sqrtf(q / (float)kDM + eps);
-    const float4 gv = *reinterpret_cast<const float4 *>(gamma + lane * 4);
-    const float4 bv = *reinterpret_cast<const float4 *>(beta + lane * 4);
+    const float scale = 1.0f / sqrtf(wave_sum(q) / (float)kDM + eps);
     const float y[4] = {v[0] * scale * gv.x + bv.x, v[1] * scale * gv.y + bv.y, v[2] * scale * gv.z + bv.z,
                         v[3] * scale * gv.w + bv.w};
     if (out_chw) {

@@ -123,6 +123,14 @@ int run_node(const int32_t *p, const ppdl_tview *dst, const ppdl_tview *src, int
 // src index of the op's optional workspace, or -1 for ops that take none
 int workspace_src_index(const int32_t *p);
 hipError_t gemm_im2col(const GemmArgs &g, const GemmWorkspace &ws, hipStream_t s);
+// Shape-fitted 16x16-MFMA GEMM for dense k-major A and B (gemm_lt.hip): no
+// workspace.  gemm_lt_pick returns a menu index or -1 (g.n_vec must be set;
+// `wanted`: the caller's planner prefers this kernel for the shape).
+bool gemm_lt_ok(const GemmArgs &g);
+int gemm_lt_pick(const GemmArgs &g, int cus, bool wanted);
+int gemm_lt_num_cfgs();
+hipError_t gemm_lt(const GemmArgs &g, int cfg, hipStream_t s);
+std::string gemm_lt_name(int cfg);
 
 // ---- Winograd transforms ----
 // pad: 0 when x is already padded (op 10), 1 when the conv's pad is fused.

@@ -199,12 +199,96 @@ def test_conv1x1_plane_strided(hip, orc, IC, H, W, OC, ld):
         srcs = [hip.chw_view(xs, W, H), dev(wr), dev(b)] + ([hip.chw_view(adds, W, H)] if mode else [])
         d = hip.chw_view(out, W, H)
         srcs = with_ws(hip, hip.OP_CONV1X1_BA, d, srcs, 1, mode, True)
-        if ld % 4 == 0 and IC >= 1024:  # the stage-3 aggregations (smaller GEMMs plan the small kernel)
-            assert hip.kernel_name(hip.OP_CONV1X1_BA, d, srcs, 1, mode).startswith("k_gemm_dma")
+        if ld % 4 == 0 and IC >= 1024:  # the stage-3 aggregations: a float4 B loader
+            assert hip.kernel_name(hip.OP_CONV1X1_BA, d, srcs, 1, mode).startswith(("k_gemm_dma", "k_gemm_lt"))
         hip.run_checked(hip.OP_CONV1X1_BA, d, srcs, 1, mode)
         y = host(out)
         assert np.isnan(y[:, P:]).all()
         assert normwise(y[:, :P], ref + add if mode else ref) < TOL
+
+
+def lt_menu(hip, op, dst, srcs, p14=0, p15=0):
+    """Indices of the 16x16-MFMA GEMM menu, read back through the kernel
+    names that PPDL_LT=<index> selects (an index past the menu falls back)."""
+    idx = []
+    for i in range(64):
+        os.environ["PPDL_LT"] = str(i)
+        try:
+            if not hip.kernel_name(op, dst, srcs, p14, p15).startswith("k_gemm_lt"):
+                break
+        finally:
+            os.environ.pop("PPDL_LT", None)
+        idx.append(i)
+    return idx
+
+
+LT_SHAPES = [  # (IC, H, W, OC, plane stride or 0, act, add mode)
+    (132, 9, 12, 52, 0, 2, 2),      # K not a multiple of the k tile, M and N not of the block
+    (40, 5, 7, 12, 36, 1, 0),       # 35 pixels in planes 36 floats apart
+    (1664, 50, 50, 512, 0, 1, 0),   # stage-2 aggregation: many k tiles, both loop halves
+    (1024, 25, 25, 384, 628, 1, 2),  # stage-3 map with padded planes
+]
+
+
+@pytest.mark.parametrize("shape", LT_SHAPES)
+def test_gemm_lt_menu_matches_oracle(hip, orc, shape, monkeypatch):
+    """Every entry of the shape-fitted 16x16-MFMA GEMM menu, pinned with
+    PPDL_LT=<index>, on 1x1 convs whose edges are ragged in M, N and K,
+    with padded channel planes, bias + act and a residual add: the result
+    matches the float64 oracle, padding columns stay untouched and repeated
+    launches are bitwise identical."""
+    IC, H, W, OC, ld, act, mode = shape
+    P = H * W
+    ld = ld or P
+    say(f"gemm_lt menu 1x1 {IC}->{OC} @{H}x{W} ld {ld}")
+    rng = np.random.default_rng(IC * 7 + OC)
+    x, w, b = conv_inputs(rng, IC, H, W, OC, 1)
+    wr, _ = hip.repack_conv(w)
+    xs = torch.full((IC, ld), float("nan"), device="cuda")
+    xs[:, :P] = dev(x.reshape(IC, P))
+    add = rng.standard_normal((OC, P)).astype(np.float32)
+    adds = torch.full((OC, ld), float("nan"), device="cuda")
+    adds[:, :P] = dev(add)
+    ref = orc.conv2d_ref(x, w, b, 1, 0, act).reshape(OC, P) + (add if mode == 2 else 0)
+    out = torch.full((OC, ld), float("nan"), device="cuda")
+    d = hip.chw_view(out, W, H)
+    srcs = [hip.chw_view(xs, W, H), dev(wr), dev(b)] + ([hip.chw_view(adds, W, H)] if mode else [])
+    menu = lt_menu(hip, hip.OP_CONV1X1_BA, d, srcs, act, mode)
+    assert len(menu) >= 8
+    for i in menu:
+        monkeypatch.setenv("PPDL_LT", str(i))
+        runs = []
+        for _ in range(2):
+            out.fill_(float("nan"))
+            hip.run_checked(hip.OP_CONV1X1_BA, d, srcs, act, mode)
+            runs.append(host(out).copy())
+        y = runs[0]
+        assert np.array_equal(runs[0], runs[1], equal_nan=True), f"entry {i}: not deterministic"
+        if ld > P:
+            assert np.isnan(y[:, P:]).all(), f"entry {i}: wrote padding"
+        assert normwise(y[:, :P], ref) < TOL, f"entry {i}"
+
+
+def test_gemm_lt_menu_on_winograd_planes(hip, orc, monkeypatch):
+    """The menu on op 12's batched products: 36 F(4,3) planes of 96 x 169 x
+    96 with plane rows padded to 172 floats; the whole conv matches the
+    oracle for every entry."""
+    IC, H, W, OC = 96, 50, 50, 96
+    rng = np.random.default_rng(12)
+    x, w, b = conv_inputs(rng, IC, H, W, OC, 3)
+    ref = orc.conv2d_ref(x, w, b, 1, 1, 1)
+    T = 13 * 13
+    _, wg4 = hip.repack_conv(w)
+    dt = torch.full((36, IC, 172), float("nan"), device="cuda")
+    yt = torch.full((36, OC, 172), float("nan"), device="cuda")
+    vdt, vyt = planes_view(hip, dt, T, IC), planes_view(hip, yt, T, OC)
+    menu = lt_menu(hip, hip.OP_WG4_MADD, vyt, [vdt, dev(wg4)])
+    assert len(menu) >= 8
+    for i in menu:
+        monkeypatch.setenv("PPDL_LT", str(i))
+        say(f"gemm_lt menu F(4,3) planes entry {i}")
+        out, _ = hip_winograd_padded(hip, x, w, b, 1, 172)
+        assert normwise(host(out), ref) < TOL, f"entry {i}"
 
 
 @pytest.mark.parametrize("wv", ["", "1", "2", "4", "8", "16"])
@@ -257,18 +341,29 @@ def test_wg4_input_vector_loads(hip, orc, IC, H, W):
 @pytest.mark.parametrize("IC,H,W,OC", [(64, 100, 100, 48), (96, 50, 50, 96), (256, 25, 25, 256), (7, 9, 11, 5)])
 def test_winograd_padded_planes(hip, orc, IC, H, W, OC):
     """dt / yt plane rows padded past T (NaN-filled padding): the padding is
-    never read into a stored output, and the result equals the contiguous
-    layout's bit for bit (same kernels, same summation order)."""
+    never read into a stored output (the result is finite), and the result
+    equals the contiguous layout's bit for bit when both layouts run the same
+    plane kernel (same summation order); padded rows whose width is whole
+    float4s may select the float4-loading kernel instead, which then agrees
+    within the tolerance."""
     say(f"F(4,3) padded planes {IC}->{OC} @{H}x{W}")
     rng = np.random.default_rng(IC + H + OC)
     x, w, b = conv_inputs(rng, IC, H, W, OC, 3)
     T = ((W + 3) // 4) * ((H + 3) // 4)
+    _, wg4 = hip.repack_conv(w)
+    packed = hip.kernel_name(hip.OP_WG4_MADD, torch.empty((36, OC, T), device="cuda"),
+                             [torch.empty((36, IC, T), device="cuda"), dev(wg4)])
     ref_out = host(hip_winograd(hip, x, w, b, 2)[0])
     for ldt in ((T + 3) // 4 * 4, T + 17):
         out, dt = hip_winograd_padded(hip, x, w, b, 2, ldt)
         y = host(out)
         assert np.isfinite(y).all()
-        assert np.array_equal(y, ref_out), ldt
+        vdt = planes_view(hip, torch.empty((36, IC, ldt), device="cuda"), T, IC)
+        vyt = planes_view(hip, torch.empty((36, OC, ldt), device="cuda"), T, OC)
+        if hip.kernel_name(hip.OP_WG4_MADD, vyt, [vdt, dev(wg4)]) == packed:
+            assert np.array_equal(y, ref_out), ldt
+        else:
+            assert normwise(y, ref_out) < TOL, ldt
         assert normwise(y, orc.conv2d_ref(x, w, b, 1, 1, 2)) < TOL
         if ldt > T:
             assert torch.isnan(dt[:, :, T:]).all().item()  # the input transform leaves the padding alone
@@ -752,6 +847,7 @@ def test_dma_tail_balancing_bit_identical(hip, orc, kind, IC, OC, H, W, monkeypa
     same k split and sum order, so bit-identical, and both at the oracle's
     tolerance."""
     say(f"tail balancing {kind} {IC}->{OC} @{H}x{W}")
+    monkeypatch.setenv("PPDL_LT", "off")  # the 64x64 kernel even if the 16x16 menu were planned
     rng = np.random.default_rng(IC + OC + W)
     outs = []
     def launched(flag, op, dst, srcs, p14=0):
