@@ -1274,9 +1274,10 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(const float *__restrict__
 // along k, the same address across a half-wave).
 constexpr int kSmallKC = 32;
 
-template <int AMODE, int WV, bool PRE>
-__global__ __launch_bounds__(WV * 64) void k_gemm_small(GemmArgs g, int tiles_m, int tiles_mn) {
+template <int AMODE, int WV, bool PRE, bool LN>
+__device__ __forceinline__ void gemm_small_body(const GemmArgs &g, int tiles_m, int tiles_mn) {
     constexpr int KC = kSmallKC, NS = KC / 2, NT = WV * 64;
+    static_assert(!LN || AMODE == 1, "the row norm prologue reads row-major A");
     __shared__ float red[WV][32][33];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int l32 = lane & 31, h = lane >> 5;
@@ -1319,7 +1320,7 @@ __global__ __launch_bounds__(WV * 64) void k_gemm_small(GemmArgs g, int tiles_m,
                 // K % 4 == 0: the 4 k are all inside or all outside
                 const uint32_t ai = (uint32_t)(mc * lda + min(k4, K - 4));
                 float4 v = ld4(A + ai);
-                if (PRE) {
+                if (PRE && !LN) {
                     const float4 p = ld4(A2 + ai);
                     v.x += pre ? p.x : 0.0f;
                     v.y += pre ? p.y : 0.0f;
@@ -1378,7 +1379,65 @@ __global__ __launch_bounds__(WV * 64) void k_gemm_small(GemmArgs g, int tiles_m,
     };
     // chunks of this wave: wave, wave + WV, ...; two register stages
     int ch = wave;
-    if (ch < nchunk) load(a0, b0, ch);
+    if (!LN && ch < nchunk) load(a0, b0, ch);
+    if constexpr (LN) {
+        // Row norm of A in the prologue (the decoder's post-residual layer
+        // norms, src/ppdoclayout.cpp:550-554): the launch gives every wave
+        // exactly one 32-k chunk, so the block holds whole rows.  Mean, then
+        // the variance of the centred values (two passes), each as lane
+        // sums + the partner half-wave + the waves' partials in wave order;
+        // y = (x - mean) / sqrt(var + 1e-5) * gamma + beta.  The blocks of
+        // the first column tile store y (ln_out, [M][K]) for later use as a
+        // residual; a_add (PRE) is added after the norm.
+        __shared__ float lsum[WV][32];
+        load(a0, b0, ch);
+        float gk[NS], bk[NS], pk[NS];
+#pragma unroll
+        for (int c = 0; c < KC / 8; c++) {
+            const int k4 = ch * KC + 8 * c + 4 * h;
+            const float4 gv = ld4(g.ln_g + k4), bv = ld4(g.ln_b + k4);
+            const float4 pv = PRE ? ld4(A2 + (uint32_t)(mc * lda + k4)) : float4{0.0f, 0.0f, 0.0f, 0.0f};
+            gk[4 * c] = gv.x, gk[4 * c + 1] = gv.y, gk[4 * c + 2] = gv.z, gk[4 * c + 3] = gv.w;
+            bk[4 * c] = bv.x, bk[4 * c + 1] = bv.y, bk[4 * c + 2] = bv.z, bk[4 * c + 3] = bv.w;
+            pk[4 * c] = pv.x, pk[4 * c + 1] = pv.y, pk[4 * c + 2] = pv.z, pk[4 * c + 3] = pv.w;
+        }
+        float s = 0.0f;
+#pragma unroll
+        for (int j = 0; j < NS; j++) s += a0[j];
+        s += __shfl_xor(s, 32);
+        if (h == 0) lsum[wave][l32] = s;
+        __syncthreads();
+        float tot = 0.0f;
+#pragma unroll
+        for (int w = 0; w < WV; w++) tot += lsum[w][l32];
+        const float mean = tot / (float)K;
+        float q = 0.0f;
+#pragma unroll
+        for (int j = 0; j < NS; j++) {
+            a0[j] -= mean;
+            q += a0[j] * a0[j];
+        }
+        q += __shfl_xor(q, 32);
+        __syncthreads();  // every wave has read the sums
+        if (h == 0) lsum[wave][l32] = q;
+        __syncthreads();
+        float qt = 0.0f;
+#pragma unroll
+        for (int w = 0; w < WV; w++) qt += lsum[w][l32];
+        const float scale = 1.0f / sqrtf(qt / (float)K + 1e-5f);
+#pragma unroll
+        for (int j = 0; j < NS; j++) a0[j] = a0[j] * scale * gk[j] + bk[j];
+        if (g.ln_out && n0 == 0 && m0 + l32 < M) {
+#pragma unroll
+            for (int c = 0; c < KC / 8; c++)
+                *reinterpret_cast<float4 *>(g.ln_out + (int64_t)(m0 + l32) * K + ch * KC + 8 * c + 4 * h) =
+                    make_float4(a0[4 * c], a0[4 * c + 1], a0[4 * c + 2], a0[4 * c + 3]);
+        }
+        if (PRE && pre) {
+#pragma unroll
+            for (int j = 0; j < NS; j++) a0[j] += pk[j];
+        }
+    }
     while (ch < nchunk) {
         if (ch + WV < nchunk) load(a1, b1, ch + WV);
         __builtin_amdgcn_sched_barrier(0);
@@ -1419,6 +1478,17 @@ __global__ __launch_bounds__(WV * 64) void k_gemm_small(GemmArgs g, int tiles_m,
             C[idx] = v;
         }
     }
+}
+
+template <int AMODE, int WV, bool PRE>
+__global__ __launch_bounds__(WV * 64) void k_gemm_small(GemmArgs g, int tiles_m, int tiles_mn) {
+    gemm_small_body<AMODE, WV, PRE, false>(g, tiles_m, tiles_mn);
+}
+
+// the small GEMM with the row-norm prologue (row-major A, K = 32 * WV)
+template <int WV, bool PRE>
+__global__ __launch_bounds__(WV * 64) void k_gemm_small_ln(GemmArgs g, int tiles_m, int tiles_mn) {
+    gemm_small_body<1, WV, PRE, true>(g, tiles_m, tiles_mn);
 }
 
 // Waves of the small-GEMM kernel (PPDL_SMALL_WV pins 4, 8 or 16 for sweeps
@@ -1679,10 +1749,36 @@ bool lt_wanted(const GemmArgs &g, const GemmPlan &p) {
     return g.batch == 1 && g.N <= 4096 && p.cfg != kCfgSmall && p.splits > 1 && g.K <= 1536;
 }
 
+// the small GEMM with the row-norm prologue: one 32-k chunk per wave
+bool ln_ok(const GemmArgs &g) {
+    const auto a16 = [](const void *q) { return (((uintptr_t)q) & 15) == 0; };
+    const int wv = g.K / kSmallKC;
+    return g.a_rowmajor && !g.a_w4 && !g.bits && g.ln_b && g.batch == 1 && g.K % kSmallKC == 0 &&
+           (wv == 8 || wv == 16) && g.lda % 4 == 0 && a16(g.A) && a16(g.ln_g) && a16(g.ln_b) &&
+           (!g.ln_out || a16(g.ln_out)) && (!g.a_add || (a16(g.a_add) && g.a_add_n % 32 == 0)) &&
+           (int64_t)g.M * g.lda < 0x7fffffff && (int64_t)g.K * g.ldb < 0x7fffffff;
+}
+
+hipError_t launch_ln(const GemmArgs &g, hipStream_t s) {
+    if (!ln_ok(g)) return hipErrorInvalidValue;
+    const int tiles_m = (g.M + 31) / 32, tiles_n = (g.N + 31) / 32, tmn = tiles_m * tiles_n;
+    const dim3 grid((unsigned)tmn);
+    const bool pre = g.a_add != nullptr;
+    if (g.K == 8 * kSmallKC) {
+        if (pre) hipLaunchKernelGGL((k_gemm_small_ln<8, true>), grid, dim3(512), 0, s, g, tiles_m, tmn);
+        else hipLaunchKernelGGL((k_gemm_small_ln<8, false>), grid, dim3(512), 0, s, g, tiles_m, tmn);
+    } else {
+        if (pre) hipLaunchKernelGGL((k_gemm_small_ln<16, true>), grid, dim3(1024), 0, s, g, tiles_m, tmn);
+        else hipLaunchKernelGGL((k_gemm_small_ln<16, false>), grid, dim3(1024), 0, s, g, tiles_m, tmn);
+    }
+    return hipGetLastError();
+}
+
 template <int BMODE>
 hipError_t dispatch(const GemmArgs &g_in, const GemmWorkspace &ws, hipStream_t s) {
     GemmArgs g = g_in;
     g.n_vec = BMODE == 0 ? n_vec_of(g) : 0;
+    if (g.ln_g) return BMODE == 0 ? launch_ln(g, s) : hipErrorInvalidValue;
     if (BMODE == 1) {
         if (const int cc = patch_cc(g)) return launch_patch(g, cc, s);
         if (direct_ok(g)) return launch_direct(g, s);
@@ -1765,7 +1861,7 @@ GemmPlan gemm_plan(const GemmArgs &g, int64_t ws_bytes, bool im2col) {
 }
 
 int64_t gemm_ws_bytes_for(const GemmArgs &g, bool im2col) {
-    if (g.a_w4) return 0;  // the small kernel, no split-K
+    if (g.a_w4 || g.ln_g) return 0;  // the small kernel, no split-K
     if (im2col && !patch_cc(g) && (direct_ok(g) || frag_ok(g))) return 0;  // neither kernel uses a workspace
     const GemmPlan p = gemm_plan(g, INT64_MAX, im2col);
     return gemm_ws_bytes(g.M, g.N, g.batch, p.cfg, p.splits);
@@ -1778,6 +1874,7 @@ std::string gemm_kernel_name(const GemmArgs &g, int64_t ws_bytes, bool im2col) {
     if (im2col && direct_ok(g)) return "k_conv_k3s2<" + std::to_string(g.IC) + ">";
     if (im2col && frag_ok(g)) return "k_conv_frag<" + std::to_string(frag_waves(g)) + ">";
     if (g.a_w4) return "k_gemm_small<2, " + std::to_string(small_waves(g.K, small_tiles(g))) + ", false>";
+    if (g.ln_g) return "k_gemm_small_ln<" + std::to_string(g.K / kSmallKC) + (g.a_add ? ", true>" : ", false>");
     const GemmPlan p = gemm_plan(g, ws_bytes, im2col);
     if (!im2col) {
         GemmArgs gv = g;

@@ -286,8 +286,11 @@ class Net {
     // 1x1 convs only, like a strided x
     Img conv(const Img &x, const std::string &name, int s, int p, int act, float *out = nullptr, int pad_end = 0,
              const float *add = nullptr, int add_mode = 0, int64_t out_ld = 0);
+    // ln: a layer norm applied to x in the GEMM's A loader, its result
+    // stored to ln_out
     Seq lin(const Seq &x, const std::string &name, int act, float *out = nullptr, const float *add = nullptr,
-            int add_mode = 0, const float *a_add = nullptr, int a_add_n = 0);
+            int add_mode = 0, const float *a_add = nullptr, int a_add_n = 0, const std::string &ln = "",
+            float *ln_out = nullptr);
     Seq ln(const Seq &a, const float *b, const std::string &name, float *out = nullptr, int out_chw = 0);
     Seq mlp3(const Seq &x, const std::string &pfx);
     Seq lin_in4(const Seq &x, const std::string &first, const std::string &second, int act);
@@ -569,7 +572,7 @@ Img Net::conv(const Img &x, const std::string &name, int s, int p, int act, floa
 // and fused add (residual) in the epilogue, and an optional prologue add
 // (x + a_add, same layout as x) for output columns < a_add_n.
 Seq Net::lin(const Seq &x, const std::string &name, int act, float *out, const float *add, int add_mode,
-             const float *a_add, int a_add_n) {
+             const float *a_add, int a_add_n, const std::string &ln, float *ln_out) {
     const auto &ne = shape(name + ".weight");  // (in, out)
     const int in = (int)ne[0], nout = (int)ne[1];
     if (in != x.D && bad_node_.empty()) bad_node_ = name + " (feature mismatch)";
@@ -593,6 +596,11 @@ Seq Net::lin(const Seq &x, const std::string &name, int act, float *out, const f
     g.add_mode = add_mode;
     g.a_add = a_add;
     g.a_add_n = a_add_n;
+    if (!ln.empty()) {
+        g.ln_g = W(ln + ".weight");
+        g.ln_b = W(ln + ".bias");
+        g.ln_out = ln_out;
+    }
     gemm(name, g);
     return y;
 }
@@ -895,27 +903,48 @@ bool Net::build(bool dumps, std::string *err) {
     // ---- decoder layers (:824-863)
     Seq ref{boxes_, NQ, 4, 4};
     Seq xq = target;
+    const char *dln = getenv("PPDL_DEC_LN");
+    const bool fused_ln = !(dln && dln[0] == '0');
     for (int i = 0; i < 6; i++) {
         const std::string dp = "dec" + std::to_string(i);
         Seq qpos = lin_in4(ref, "qpos.0", "qpos.1", kActNone);
-        Seq sa = mha(xq, qpos.d, dp + ".sa", nullptr, xq.d);  // x + attn, q = k = x + qpos
-        xq = ln(sa, nullptr, dp + ".ln1");
+        // The post-residual layer norms (ln1..ln3) run in the A loader of the
+        // GEMM that consumes them, which also stores the normed rows for
+        // the residual add two GEMMs later: no layer-norm launches
+        // (PPDL_DEC_LN=0: separate layer-norm launches, for A/B runs).
+        // lnz(z, norm, out): out = norm(z) as its own launch, or nothing
+        // here and the norm's name for the consumer's loader.
+        auto lnz = [&](const Seq &z, const std::string &norm, Seq &out) -> std::string {
+            if (!fused_ln) {
+                ln(z, nullptr, norm, out.d);
+                return "";
+            }
+            return norm;
+        };
+        Seq sa = mha(xq, qpos.d, dp + ".sa", nullptr, xq.d);  // z1 = x + attn, q = k = x + qpos
+        Seq x1{alloc((int64_t)NQ * kDM), NQ, kDM, kDM};       // ln1(z1)
+        const std::string n1 = lnz(sa, dp + ".ln1", x1);
         if (i == 0) join(2);
-        // sampling offsets | attention logits of (x + qpos), one [NQ][288] GEMM
-        Seq soaw = lin(xq, dp + ".ca.soaw", kActNone, nullptr, nullptr, 0, qpos.d, 1 << 30);
+        // sampling offsets | attention logits of (ln1(z1) + qpos), one [NQ][288] GEMM
+        Seq soaw = lin(fused_ln ? sa : x1, dp + ".ca.soaw", kActNone, nullptr, nullptr, 0, qpos.d, 1 << 30, n1, x1.d);
         Seq ca{alloc((int64_t)NQ * kDM), NQ, kDM, kDM};
         tagged(dp + ".msdeform", PPDL_OP_MSDEF, 0, 0, view(ca.d, {kDM, NQ}),
                {row_view(vcat.d + (int64_t)i * kDM, kDM, NTOK, vcat.ld), row_view(soaw.d, 192, NQ, soaw.ld),
                 row_view(soaw.d + 192, 96, NQ, soaw.ld), view(ref.d, {4, NQ})});
-        Seq cao = lin(ca, dp + ".ca.op", kActNone, nullptr, xq.d, 2);  // x + ca
-        xq = ln(cao, nullptr, dp + ".ln2");
-        Seq ff = lin(lin(xq, dp + ".fc1", kActRelu), dp + ".fc2", kActNone, nullptr, xq.d, 2);
-        xq = ln(ff, nullptr, dp + ".ln3");
-        static const char *hn[6] = {"hidden0", "hidden1", "hidden2", "hidden3", "hidden4", "hidden5"};
-        dump(hn[i], xq.d, {kDM, NQ});
+        Seq cao = lin(ca, dp + ".ca.op", kActNone, nullptr, x1.d, 2);  // z2 = x1 + ca
+        Seq x2{alloc((int64_t)NQ * kDM), NQ, kDM, kDM};                // ln2(z2)
+        const std::string n2 = lnz(cao, dp + ".ln2", x2);
+        Seq h1 = lin(fused_ln ? cao : x2, dp + ".fc1", kActRelu, nullptr, nullptr, 0, nullptr, 0, n2, x2.d);
+        Seq ff = lin(h1, dp + ".fc2", kActNone, nullptr, x2.d, 2);  // z3 = x2 + ffn
+        Seq x3{alloc((int64_t)NQ * kDM), NQ, kDM, kDM};             // ln3(z3): the layer's output
+        const std::string n3 = lnz(ff, dp + ".ln3", x3);
         // box refinement ref = sigmoid(delta + inv_sigmoid(ref)) in the last
         // bbox-head GEMM's epilogue, in place
-        Seq bh = lin(lin(xq, "bbox_head.0", kActRelu), "bbox_head.1", kActRelu);
+        Seq bh0 = lin(fused_ln ? ff : x3, "bbox_head.0", kActRelu, nullptr, nullptr, 0, nullptr, 0, n3, x3.d);
+        xq = x3;
+        static const char *hn[6] = {"hidden0", "hidden1", "hidden2", "hidden3", "hidden4", "hidden5"};
+        dump(hn[i], xq.d, {kDM, NQ});
+        Seq bh = lin(bh0, "bbox_head.1", kActRelu);
         lin(bh, "bbox_head.2", kActNone, boxes_, boxes_, 3);
     }
 

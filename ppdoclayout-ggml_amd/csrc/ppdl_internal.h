@@ -89,6 +89,13 @@ struct GemmArgs {
     // 0): with bits set the results are not stored; bit n % 32 of word
     // bits[m * (N / 32) + n / 32] is (acc > 0), before any bias or act.
     uint32_t *bits;
+    // Row-norm prologue (small-GEMM kernel, row-major A, K = 256 or 512):
+    // with ln_g set, the A operand is LN(A) * ln_g + ln_b per row (layer
+    // norm, eps 1e-5) before any a_add, and when ln_out is set the normed
+    // rows are also stored there ([M][K], token-major).
+    const float *ln_g;
+    const float *ln_b;
+    float *ln_out;
 };
 
 // act codes of the GEMM epilogue and the elementwise kernels
