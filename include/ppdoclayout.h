@@ -98,6 +98,10 @@ typedef struct {
 } ppdl_node_stat;
 
 /* Fills out[0..n) for the first min(cap, nodes) nodes; returns n or -1.
+ * iters > 0: each node alone, captured iters times into a graph of its own.
+ * iters < 0: the whole graph captured once with a wall-clock stamp kernel
+ * after every node and replayed -iters times; `us` is then the node's mean
+ * share of a replay in context, less the interval of an empty stamp pair.
  * Intermediate buffers are left in an arbitrary state (the next ppdl_infer or
  * ppdl_compute recomputes them). */
 PPDL_API int ppdl_profile_nodes(ppdl_ctx * ctx, int iters, ppdl_node_stat * out, int cap);

@@ -145,6 +145,7 @@ class Net {
     int replay();  // one graph launch + sync
     double time_graph(int iters);
     int profile_nodes(int iters, ppdl_node_stat *out, int cap);
+    int profile_in_graph(int reps, ppdl_node_stat *out, int cap);
     bool upload_image(const float *host);
     // the host result's inputs: mask sign bits packed on the device, then
     // logits, boxes, order and the bits copied into pinned buffers
@@ -1124,7 +1125,67 @@ double Net::time_graph(int iters) {
 // the host's per-launch cost, several µs, to every short kernel.)  Nodes that
 // update a buffer in place drift its contents meanwhile; the next ppdl_infer /
 // ppdl_compute recomputes everything from the image.
+// In-graph mode (iters < 0): the whole node list captured once into one
+// graph with a one-lane kernel storing the device wall clock in front of it
+// and after every kernel node, replayed -iters times; a node's time is the
+// mean interval between its stamp and the previous one, less the interval
+// of two stamps with nothing between them: its share of a replay in context
+// (operands as the previous nodes left them).  One stream only.
+int Net::profile_in_graph(int reps, ppdl_node_stat *out, int cap) {
+    if (multi_lane_ || reps < 1) return -1;
+    std::vector<size_t> idx;
+    for (size_t i = 0; i < nodes_.size(); i++)
+        if (nodes_[i].kind == 0) idx.push_back(i);
+    const size_t ns = idx.size() + 2;  // stamps: front, after each node, one more for the baseline
+    unsigned long long *dstamp = nullptr;
+    int khz = 0;
+    bool good = hipMalloc((void **)&dstamp, ns * sizeof(unsigned long long)) == hipSuccess &&
+                hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, 0) == hipSuccess && khz > 0;
+    hipGraph_t g = nullptr;
+    hipGraphExec_t ge = nullptr;
+    if (good) {
+        good = hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal) == hipSuccess;
+        bool ran = good && stamp(dstamp, stream_) == hipSuccess;
+        for (size_t k = 0; ran && k < idx.size(); k++)
+            ran = nodes_[idx[k]].run(stream_) == 0 && stamp(dstamp + k + 1, stream_) == hipSuccess;
+        ran = ran && stamp(dstamp + idx.size() + 1, stream_) == hipSuccess;
+        good = good && hipStreamEndCapture(stream_, &g) == hipSuccess && ran;  // capture always ended
+        good = good && hipGraphInstantiate(&ge, g, nullptr, nullptr, 0) == hipSuccess;
+    }
+    std::vector<unsigned long long> h(ns);
+    std::vector<double> acc(idx.size(), 0.0);
+    double base = 0.0;
+    good = good && hipGraphLaunch(ge, stream_) == hipSuccess && hipStreamSynchronize(stream_) == hipSuccess;
+    for (int r = 0; good && r < reps; r++) {
+        good = hipGraphLaunch(ge, stream_) == hipSuccess && hipStreamSynchronize(stream_) == hipSuccess &&
+               hipMemcpy(h.data(), dstamp, ns * sizeof(unsigned long long), hipMemcpyDeviceToHost) == hipSuccess;
+        for (size_t k = 0; good && k < idx.size(); k++) acc[k] += (double)(h[k + 1] - h[k]);
+        base += (double)(h[ns - 1] - h[ns - 2]);
+    }
+    if (ge) (void)hipGraphExecDestroy(ge);
+    if (g) (void)hipGraphDestroy(g);
+    if (dstamp) (void)hipFree(dstamp);
+    if (!good) return -1;
+    const double us_per_tick = 1000.0 / khz;
+    base = base / reps * us_per_tick;
+    int n = 0;
+    for (size_t k = 0; k < idx.size() && n < cap; k++) {
+        const Node &nd = nodes_[idx[k]];
+        ppdl_node_stat &o = out[n++];
+        memset(&o, 0, sizeof(o));
+        snprintf(o.name, sizeof(o.name), "%s", nd.name.c_str());
+        snprintf(o.kernel, sizeof(o.kernel), "%s", nd.kern.c_str());
+        o.cls = nd.cls;
+        o.kernels = nd.kernels;
+        o.flops = nd.flops;
+        o.bytes = nd.bytes;
+        o.us = acc[k] / reps * us_per_tick - base;
+    }
+    return n;
+}
+
 int Net::profile_nodes(int iters, ppdl_node_stat *out, int cap) {
+    if (iters < 0) return profile_in_graph(-iters, out, cap);
     hipEvent_t e0, e1;
     if (iters < 1 || hipEventCreate(&e0) != hipSuccess) return -1;
     if (hipEventCreate(&e1) != hipSuccess) {

@@ -16,6 +16,8 @@ hipError_t interp(const float *x, const float *add, float *out, int C, int IH, i
                   int bilinear, hipStream_t s);
 // out = LN(a + b) over 256 features per token (b may be null); out_chw
 // writes [256][T] instead of [T][256]
+// slot = the device wall clock when the kernel runs (in-graph profiling)
+hipError_t stamp(unsigned long long *slot, hipStream_t s);
 hipError_t layernorm(const float *a, const float *b, const float *gamma, const float *beta, float *out, int T,
                      int out_chw, hipStream_t s);
 // 8-head x 32 attention over token-major q/k/v (row strides in floats)

@@ -228,10 +228,12 @@ __global__ __launch_bounds__(256) void k_layernorm(const float *__restrict__ a, 
 // lane pair, and the accumulator registers of S^T are directly the B operand
 // of O^T += V^T P^T (register r holds keys 8(r/4) + r%4 in lanes 0-31 and 4
 // more in lanes 32-63, which fixes the key each lane supplies on the A side).
-// K and V chunks pass through a per-wave LDS slice; no block barrier until
-// the merge.
+// K and V chunks pass through a per-wave LDS slice; a wave issues the loads
+// of all its chunks (at most kAttCPW) before the first one's math.  The
+// block's Q goes through LDS once; after that barrier, none until the merge.
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 constexpr int kAttQ = 32, kAttWaves = 8, kAttThreads = 64 * kAttWaves;
+constexpr int kAttCPW = 3;  // key chunks per wave held in registers: T <= 8 * 3 * 32 = 768
 
 __global__ __launch_bounds__(kAttThreads) void k_attention(const float *__restrict__ q, int ldq,
                                                            const float *__restrict__ k, int ldk,
@@ -246,39 +248,61 @@ __global__ __launch_bounds__(kAttThreads) void k_attention(const float *__restri
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int l32 = lane & 31, hi = lane >> 5;
 
-    // B operand of S^T: Q^T[d][q], lane supplies d = 2*st + hi of query l32
-    float qf[kHD / 2];
-    {
-        const int t = q0 + l32;
-        const float *qr = q + (int64_t)min(t, T - 1) * ldq + h * kHD + hi;
+    // This wave's K/V chunks (c = wave, wave + 8, ...; at most kAttCPW), all
+    // of their loads issued before any math: lane = key row lane/2, 16
+    // consecutive channels (lane%2)*16; rows past T read row T - 1 and are
+    // zeroed when staged.
+    const int row = lane >> 1, c0 = (lane & 1) * 16;
+    float4 kv[kAttCPW][8];
 #pragma unroll
-        for (int st = 0; st < kHD / 2; st++) qf[st] = t < T ? qr[2 * st] : 0.0f;
+    for (int u = 0; u < kAttCPW; u++) {
+        const int s_ = min((wave + kAttWaves * u) * 32 + row, T - 1);
+        const float4 *kr = reinterpret_cast<const float4 *>(k + (int64_t)s_ * ldk + h * kHD + c0);
+        const float4 *vr = reinterpret_cast<const float4 *>(v + (int64_t)s_ * ldv + h * kHD + c0);
+#pragma unroll
+        for (int j = 0; j < 4; j++) kv[u][j] = kr[j], kv[u][4 + j] = vr[j];
     }
+    // Q of the block's 32 queries through LDS (one float4 per thread of
+    // the first four waves), read back as the B operand of S^T: Q^T[d][q],
+    // lane supplies d = 2*st + hi of query l32
+    __shared__ float qs[kAttQ][kHD + 1];
+    if (threadIdx.x < kAttQ * kHD / 4) {
+        const int qi = threadIdx.x >> 3, d4 = (threadIdx.x & 7) * 4;
+        const float4 qv =
+            *reinterpret_cast<const float4 *>(q + (int64_t)min(q0 + qi, T - 1) * ldq + h * kHD + d4);
+        const bool in = q0 + qi < T;
+        qs[qi][d4 + 0] = in ? qv.x : 0.0f;
+        qs[qi][d4 + 1] = in ? qv.y : 0.0f;
+        qs[qi][d4 + 2] = in ? qv.z : 0.0f;
+        qs[qi][d4 + 3] = in ? qv.w : 0.0f;
+    }
+    __syncthreads();
+    float qf[kHD / 2];
+#pragma unroll
+    for (int st = 0; st < kHD / 2; st++) qf[st] = qs[l32][2 * st + hi];
     f32x16_t o;
 #pragma unroll
     for (int r = 0; r < 16; r++) o[r] = 0.0f;
     float m = -INFINITY, lsum = 0.0f;
 
-    for (int c = wave; c * 32 < T; c += kAttWaves) {
+#pragma unroll
+    for (int u = 0; u < kAttCPW; u++) {
+        const int c = wave + kAttWaves * u;
+        if (c * 32 >= T) break;  // wave-uniform
         const int key0 = c * 32;
         {
-            // lane: key row lane/2, 16 consecutive channels (lane%2)*16
-            const int row = lane >> 1, c0 = (lane & 1) * 16, s_ = key0 + row;
-            const bool in = s_ < T;
-            const float4 *kr = reinterpret_cast<const float4 *>(k + (int64_t)min(s_, T - 1) * ldk + h * kHD + c0);
-            const float4 *vr = reinterpret_cast<const float4 *>(v + (int64_t)min(s_, T - 1) * ldv + h * kHD + c0);
+            const bool in = key0 + row < T;
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                float4 a = kr[j], b = vr[j];
-                if (!in) a = b = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-                Ks[wave][row][c0 + 4 * j + 0] = a.x;
-                Ks[wave][row][c0 + 4 * j + 1] = a.y;
-                Ks[wave][row][c0 + 4 * j + 2] = a.z;
-                Ks[wave][row][c0 + 4 * j + 3] = a.w;
-                Vs[wave][row][c0 + 4 * j + 0] = b.x;
-                Vs[wave][row][c0 + 4 * j + 1] = b.y;
-                Vs[wave][row][c0 + 4 * j + 2] = b.z;
-                Vs[wave][row][c0 + 4 * j + 3] = b.w;
+                const float4 a = kv[u][j], b = kv[u][4 + j];
+                Ks[wave][row][c0 + 4 * j + 0] = in ? a.x : 0.0f;
+                Ks[wave][row][c0 + 4 * j + 1] = in ? a.y : 0.0f;
+                Ks[wave][row][c0 + 4 * j + 2] = in ? a.z : 0.0f;
+                Ks[wave][row][c0 + 4 * j + 3] = in ? a.w : 0.0f;
+                Vs[wave][row][c0 + 4 * j + 0] = in ? b.x : 0.0f;
+                Vs[wave][row][c0 + 4 * j + 1] = in ? b.y : 0.0f;
+                Vs[wave][row][c0 + 4 * j + 2] = in ? b.z : 0.0f;
+                Vs[wave][row][c0 + 4 * j + 3] = in ? b.w : 0.0f;
             }
         }
         __builtin_amdgcn_wave_barrier();
@@ -459,6 +483,17 @@ hipError_t interp(const float *x, const float *add, float *out, int C, int IH, i
     return hipGetLastError();
 }
 
+// One lane stores the device's constant-rate wall clock (profiling only; a
+// vector store from a register).
+__global__ void k_stamp(unsigned long long *slot) {
+    if (threadIdx.x == 0) *slot = wall_clock64();
+}
+
+hipError_t stamp(unsigned long long *slot, hipStream_t s) {
+    hipLaunchKernelGGL(k_stamp, dim3(1), dim3(64), 0, s, slot);
+    return hipGetLastError();
+}
+
 hipError_t layernorm(const float *a, const float *b, const float *gamma, const float *beta, float *out, int T,
                      int out_chw, hipStream_t s) {
     // rows, gamma, beta and (token-major) out are accessed as float4
@@ -470,8 +505,10 @@ hipError_t layernorm(const float *a, const float *b, const float *gamma, const f
 
 hipError_t attention(const float *q, int ldq, const float *k, int ldk, const float *v, int ldv, float *out,
                      int ldo, int T, hipStream_t s) {
-    // K and V rows are read as float4
-    if (T < 1 || ldk % 4 || ldv % 4 || (((uintptr_t)k | (uintptr_t)v) & 15)) return hipErrorInvalidValue;
+    // K, V and Q rows are read as float4; every key chunk fits the waves' registers
+    if (T < 1 || T > kAttWaves * kAttCPW * 32 || ldk % 4 || ldv % 4 || ldq % 4 ||
+        (((uintptr_t)k | (uintptr_t)v | (uintptr_t)q) & 15))
+        return hipErrorInvalidValue;
     hipLaunchKernelGGL(k_attention, dim3((T + kAttQ - 1) / kAttQ, kNH), dim3(kAttThreads), 0, s, q, ldq, k, ldk, v, ldv,
                        out, ldo, T, 1.0f / sqrtf((float)kHD));
     return hipGetLastError();
