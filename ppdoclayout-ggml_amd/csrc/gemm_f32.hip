@@ -1273,6 +1273,7 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(const float *__restrict__
 // (its row is one float4 per lane, loaded once; W4 and b4 are read as float4
 // along k, the same address across a half-wave).
 constexpr int kSmallKC = 32;
+typedef float f32x4_small __attribute__((ext_vector_type(4)));
 
 template <int AMODE, int WV, bool PRE, bool LN>
 __device__ __forceinline__ void gemm_small_body(const GemmArgs &g, int tiles_m, int tiles_mn) {
@@ -1478,6 +1479,130 @@ __device__ __forceinline__ void gemm_small_body(const GemmArgs &g, int tiles_m, 
             C[idx] = v;
         }
     }
+}
+
+// The small GEMM in 16 x 32 tiles (two 16x16 blocks, v_mfma_f32_16x16x4f32)
+// for the decoder's long-K linears (fc2 K = 1024, the query-position MLP
+// K = 512), whose 300 x 256 outputs make only 80 tiles of 32 x 32: twice the
+// blocks, half the serial matrix work per CU.  Row-major A (AMODE 1) or the
+// computed relu(X W4 + b4) (AMODE 2); K % 32 == 0.  Within a 32-k chunk,
+// lane group g = l/16 holds k = kb + 8g .. kb + 8g + 7 of its row (two
+// float4 loads) and step j contracts k = kb + j, kb + 8 + j, kb + 16 + j,
+// kb + 24 + j (group g supplies the g-th of them); B uses the same pairing.
+// The WV waves' partial tiles are summed through LDS in wave order.
+template <int AMODE, int WV>
+__global__ __launch_bounds__(WV * 64) void k_gemm_small16(GemmArgs g, int tiles_m, int tiles_mn) {
+    constexpr int KC = kSmallKC, NT = WV * 64;
+    __shared__ float red[WV][16][33];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int l16 = lane & 15, grp = lane >> 4;
+    const int logical = xcd_remap(blockIdx.x, gridDim.x);
+    const int bz = logical / tiles_mn;
+    const int t = logical - bz * tiles_mn;
+    const int m0 = (t % tiles_m) * 16, n0 = (t / tiles_m) * 32;
+    const int M = g.M, N = g.N, K = g.K;
+    const int lda = (int)g.lda, ldb = (int)g.ldb;
+    const float *__restrict__ A = g.A + (int64_t)bz * g.sA;
+    const float *__restrict__ B = g.B + (int64_t)bz * g.sB;
+    const int mc = min(m0 + l16, M - 1), nc0 = min(n0 + l16, N - 1), nc1 = min(n0 + 16 + l16, N - 1);
+    const int nchunk = K / KC;
+    const float4 xr = AMODE == 2 ? ld4(A + (uint32_t)(mc * lda)) : float4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    auto load = [&](float (&a)[8], float (&b0)[8], float (&b1)[8], int ch) {
+        const int k8 = ch * KC + 8 * grp;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const int k4 = k8 + 4 * h;
+            if (AMODE == 2) {
+                const float4 w0 = ld4(g.a_w4 + k4), w1 = ld4(g.a_w4 + K + k4);
+                const float4 w2 = ld4(g.a_w4 + 2 * K + k4), w3 = ld4(g.a_w4 + 3 * K + k4);
+                const float4 bb = ld4(g.a_b4 + k4);
+                a[4 * h + 0] = fmaxf(fmaf(xr.w, w3.x, fmaf(xr.z, w2.x, fmaf(xr.y, w1.x, fmaf(xr.x, w0.x, bb.x)))), 0.0f);
+                a[4 * h + 1] = fmaxf(fmaf(xr.w, w3.y, fmaf(xr.z, w2.y, fmaf(xr.y, w1.y, fmaf(xr.x, w0.y, bb.y)))), 0.0f);
+                a[4 * h + 2] = fmaxf(fmaf(xr.w, w3.z, fmaf(xr.z, w2.z, fmaf(xr.y, w1.z, fmaf(xr.x, w0.z, bb.z)))), 0.0f);
+                a[4 * h + 3] = fmaxf(fmaf(xr.w, w3.w, fmaf(xr.z, w2.w, fmaf(xr.y, w1.w, fmaf(xr.x, w0.w, bb.w)))), 0.0f);
+            } else {
+                const float4 v = ld4(A + (uint32_t)(mc * lda + k4));
+                a[4 * h + 0] = v.x, a[4 * h + 1] = v.y, a[4 * h + 2] = v.z, a[4 * h + 3] = v.w;
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            b0[j] = B[(uint32_t)((k8 + j) * ldb + nc0)];
+            b1[j] = B[(uint32_t)((k8 + j) * ldb + nc1)];
+        }
+    };
+    f32x4_small acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
+    auto mma = [&](const float (&a)[8], const float (&b0)[8], const float (&b1)[8]) {
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(a[j], b0[j], acc0, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(a[j], b1[j], acc1, 0, 0, 0);
+        }
+    };
+    float a0[8], p0[8], q0[8], a1[8], p1[8], q1[8];
+    int ch = wave;
+    if (ch < nchunk) load(a0, p0, q0, ch);
+    while (ch < nchunk) {
+        if (ch + WV < nchunk) load(a1, p1, q1, ch + WV);
+        __builtin_amdgcn_sched_barrier(0);
+        mma(a0, p0, q0);
+        __builtin_amdgcn_sched_barrier(0);
+        ch += WV;
+        if (ch >= nchunk) break;
+        if (ch + WV < nchunk) load(a0, p0, q0, ch + WV);
+        __builtin_amdgcn_sched_barrier(0);
+        mma(a1, p1, q1);
+        __builtin_amdgcn_sched_barrier(0);
+        ch += WV;
+    }
+    // result register r of lane l: row 4*(l/16) + r, column l%16 of its block
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        red[wave][4 * grp + r][l16] = acc0[r];
+        red[wave][4 * grp + r][16 + l16] = acc1[r];
+    }
+    __syncthreads();
+    float *__restrict__ C = g.C + (int64_t)bz * g.sC;
+    const float *__restrict__ Ad = g.add ? g.add + (int64_t)bz * g.sC : nullptr;
+    for (int e = tid; e < 16 * 32; e += NT) {
+        const int mm = e >> 5, nn = e & 31, m = m0 + mm, n = n0 + nn;
+        if (m < M && n < N) {
+            float v = red[0][mm][nn];
+#pragma unroll
+            for (int w = 1; w < WV; w++) v += red[w][mm][nn];
+            const int64_t idx = (int64_t)m * g.ldc + n;
+            if (g.bias) v += g.bias[g.bias_n ? n : m];
+            if (g.add_mode == 1) v += Ad[idx];
+            v = act_f(v, g.act);
+            if (g.add_mode == 2) v += Ad[idx];
+            else if (g.add_mode == 3) v = refine_box(v, Ad[idx]);
+            C[idx] = v;
+        }
+    }
+}
+
+// The 16 x 32 small GEMM where the 32 x 32 one would leave fewer than 128
+// blocks for a K of at least 512 (PPDL_SMALL16=0 turns it off; read per call).
+bool small16_ok(const GemmArgs &g, int amode) {
+    const char *e = getenv("PPDL_SMALL16");
+    if (e && e[0] == '0') return false;
+    const int64_t t32 = (int64_t)((g.M + 31) / 32) * ((g.N + 31) / 32) * g.batch;
+    const auto a16 = [](const void *q) { return (((uintptr_t)q) & 15) == 0; };
+    return (amode == 1 || amode == 2) && g.K >= 512 && g.K % kSmallKC == 0 && t32 < 128 && !g.c_trans && !g.bits &&
+           !g.a_add && !g.ln_g && g.lda % 4 == 0 && a16(g.A) &&
+           (int64_t)g.M * g.lda + g.K < 0x7fffffff && (int64_t)g.K * g.ldb + g.N < 0x7fffffff;
+}
+
+hipError_t launch_small16(const GemmArgs &g, int amode, hipStream_t s) {
+    const int tiles_m = (g.M + 15) / 16, tiles_n = (g.N + 31) / 32, tmn = tiles_m * tiles_n;
+    const int64_t total = (int64_t)tmn * g.batch;
+    if (total <= 0 || total > 0x7fffffff) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)total);
+    // 8 waves with the computed A (16 would cap each wave at 128 registers: spills)
+    if (amode == 2) hipLaunchKernelGGL((k_gemm_small16<2, 8>), grid, dim3(512), 0, s, g, tiles_m, tmn);
+    else hipLaunchKernelGGL((k_gemm_small16<1, 16>), grid, dim3(1024), 0, s, g, tiles_m, tmn);
+    return hipGetLastError();
 }
 
 template <int AMODE, int WV, bool PRE>
@@ -1724,6 +1849,8 @@ hipError_t launch_small_wv(const GemmArgs &g, int wv, dim3 grid, int tiles_m, in
 
 template <int AMODE>
 hipError_t launch_small(const GemmArgs &g, hipStream_t s) {
+    if constexpr (AMODE != 0)
+        if (small16_ok(g, AMODE)) return launch_small16(g, AMODE, s);
     const int tiles_m = (g.M + 31) / 32, tiles_n = (g.N + 31) / 32;
     const int64_t total = (int64_t)tiles_m * tiles_n * g.batch;
     const int64_t a_ext = AMODE == 0 ? (int64_t)g.K * g.lda : (int64_t)g.M * g.lda;
@@ -1873,6 +2000,7 @@ std::string gemm_kernel_name(const GemmArgs &g, int64_t ws_bytes, bool im2col) {
     if (im2col && patch_cc(g)) return g.KW == 3 ? "k_conv_patch<3, 2>" : "k_conv_patch<2, 1>";
     if (im2col && direct_ok(g)) return "k_conv_k3s2<" + std::to_string(g.IC) + ">";
     if (im2col && frag_ok(g)) return "k_conv_frag<" + std::to_string(frag_waves(g)) + ">";
+    if (g.a_w4 && small16_ok(g, 2)) return "k_gemm_small16<2, 8>";
     if (g.a_w4) return "k_gemm_small<2, " + std::to_string(small_waves(g.K, small_tiles(g))) + ", false>";
     if (g.ln_g) return "k_gemm_small_ln<" + std::to_string(g.K / kSmallKC) + (g.a_add ? ", true>" : ", false>");
     const GemmPlan p = gemm_plan(g, ws_bytes, im2col);
@@ -1882,6 +2010,7 @@ std::string gemm_kernel_name(const GemmArgs &g, int64_t ws_bytes, bool im2col) {
         const int lc = gemm_lt_pick(gv, 8 * cus_per_xcd(), lt_wanted(gv, p));
         if (lc >= 0) return gemm_lt_name(lc);
     }
+    if (p.cfg == kCfgSmall && g.a_rowmajor && small16_ok(g, 1)) return "k_gemm_small16<1, 16>";
     if (p.cfg == kCfgSmall)
         return std::string("k_gemm_small<") + (g.a_rowmajor ? "1, " : "0, ") +
                std::to_string(small_waves(g.K, small_tiles(g))) + (g.a_add && g.a_rowmajor ? ", true>" : ", false>");
