@@ -1490,9 +1490,10 @@ __device__ __forceinline__ void gemm_small_body(const GemmArgs &g, int tiles_m, 
 // float4 loads) and step j contracts k = kb + j, kb + 8 + j, kb + 16 + j,
 // kb + 24 + j (group g supplies the g-th of them); B uses the same pairing.
 // The WV waves' partial tiles are summed through LDS in wave order.
-template <int AMODE, int WV>
+template <int AMODE, int WV, bool LN, bool PRE>
 __global__ __launch_bounds__(WV * 64) void k_gemm_small16(GemmArgs g, int tiles_m, int tiles_mn) {
     constexpr int KC = kSmallKC, NT = WV * 64;
+    static_assert(!(LN || PRE) || AMODE == 1, "norm and prologue add read row-major A");
     __shared__ float red[WV][16][33];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int l16 = lane & 15, grp = lane >> 4;
@@ -1507,6 +1508,10 @@ __global__ __launch_bounds__(WV * 64) void k_gemm_small16(GemmArgs g, int tiles_
     const int mc = min(m0 + l16, M - 1), nc0 = min(n0 + l16, N - 1), nc1 = min(n0 + 16 + l16, N - 1);
     const int nchunk = K / KC;
     const float4 xr = AMODE == 2 ? ld4(A + (uint32_t)(mc * lda)) : float4{0.0f, 0.0f, 0.0f, 0.0f};
+    // prologue add (row-major A): a_add has A's layout; whole 32-column
+    // tiles at or past a_add_n skip it
+    const float *__restrict__ A2 = PRE ? g.a_add + (int64_t)bz * g.sA : nullptr;
+    const bool pre = PRE && n0 < g.a_add_n;
 
     auto load = [&](float (&a)[8], float (&b0)[8], float (&b1)[8], int ch) {
         const int k8 = ch * KC + 8 * grp;
@@ -1522,7 +1527,14 @@ __global__ __launch_bounds__(WV * 64) void k_gemm_small16(GemmArgs g, int tiles_
                 a[4 * h + 2] = fmaxf(fmaf(xr.w, w3.z, fmaf(xr.z, w2.z, fmaf(xr.y, w1.z, fmaf(xr.x, w0.z, bb.z)))), 0.0f);
                 a[4 * h + 3] = fmaxf(fmaf(xr.w, w3.w, fmaf(xr.z, w2.w, fmaf(xr.y, w1.w, fmaf(xr.x, w0.w, bb.w)))), 0.0f);
             } else {
-                const float4 v = ld4(A + (uint32_t)(mc * lda + k4));
+                float4 v = ld4(A + (uint32_t)(mc * lda + k4));
+                if (PRE && !LN) {
+                    const float4 p = ld4(A2 + (uint32_t)(mc * lda + k4));
+                    v.x += pre ? p.x : 0.0f;
+                    v.y += pre ? p.y : 0.0f;
+                    v.z += pre ? p.z : 0.0f;
+                    v.w += pre ? p.w : 0.0f;
+                }
                 a[4 * h + 0] = v.x, a[4 * h + 1] = v.y, a[4 * h + 2] = v.z, a[4 * h + 3] = v.w;
             }
         }
@@ -1542,7 +1554,62 @@ __global__ __launch_bounds__(WV * 64) void k_gemm_small16(GemmArgs g, int tiles_
     };
     float a0[8], p0[8], q0[8], a1[8], p1[8], q1[8];
     int ch = wave;
-    if (ch < nchunk) load(a0, p0, q0, ch);
+    if (!LN && ch < nchunk) load(a0, p0, q0, ch);
+    if constexpr (LN) {
+        // the row norm of the small GEMM's prologue, on 16-row tiles: every
+        // wave holds one 32-k chunk of the 16 rows (the launch gives
+        // nchunk == WV); lane sums, the row's four lane groups (xor 16, 32),
+        // then the waves' partials in wave order; two passes
+        __shared__ float lsum[WV][16];
+        load(a0, p0, q0, ch);
+        const int k8 = ch * KC + 8 * grp;
+        float gk[8], bk[8], pk[8];
+#pragma unroll
+        for (int hh = 0; hh < 2; hh++) {
+            const float4 gv = ld4(g.ln_g + k8 + 4 * hh), bv = ld4(g.ln_b + k8 + 4 * hh);
+            const float4 pv = PRE ? ld4(A2 + (uint32_t)(mc * lda + k8 + 4 * hh)) : float4{0.0f, 0.0f, 0.0f, 0.0f};
+            gk[4 * hh] = gv.x, gk[4 * hh + 1] = gv.y, gk[4 * hh + 2] = gv.z, gk[4 * hh + 3] = gv.w;
+            bk[4 * hh] = bv.x, bk[4 * hh + 1] = bv.y, bk[4 * hh + 2] = bv.z, bk[4 * hh + 3] = bv.w;
+            pk[4 * hh] = pv.x, pk[4 * hh + 1] = pv.y, pk[4 * hh + 2] = pv.z, pk[4 * hh + 3] = pv.w;
+        }
+        float sm = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; j++) sm += a0[j];
+        sm += __shfl_xor(sm, 16);
+        sm += __shfl_xor(sm, 32);
+        if (grp == 0) lsum[wave][l16] = sm;
+        __syncthreads();
+        float tot = 0.0f;
+#pragma unroll
+        for (int w = 0; w < WV; w++) tot += lsum[w][l16];
+        const float mean = tot / (float)K;
+        float qq = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            a0[j] -= mean;
+            qq += a0[j] * a0[j];
+        }
+        qq += __shfl_xor(qq, 16);
+        qq += __shfl_xor(qq, 32);
+        __syncthreads();  // every wave has read the sums
+        if (grp == 0) lsum[wave][l16] = qq;
+        __syncthreads();
+        float qt = 0.0f;
+#pragma unroll
+        for (int w = 0; w < WV; w++) qt += lsum[w][l16];
+        const float scale = 1.0f / sqrtf(qt / (float)K + 1e-5f);
+#pragma unroll
+        for (int j = 0; j < 8; j++) a0[j] = a0[j] * scale * gk[j] + bk[j];
+        if (g.ln_out && n0 == 0 && m0 + l16 < M) {
+            float *o = g.ln_out + (int64_t)(m0 + l16) * K + k8;
+            *reinterpret_cast<float4 *>(o) = make_float4(a0[0], a0[1], a0[2], a0[3]);
+            *reinterpret_cast<float4 *>(o + 4) = make_float4(a0[4], a0[5], a0[6], a0[7]);
+        }
+        if (PRE && pre) {
+#pragma unroll
+            for (int j = 0; j < 8; j++) a0[j] += pk[j];
+        }
+    }
     while (ch < nchunk) {
         if (ch + WV < nchunk) load(a1, p1, q1, ch + WV);
         __builtin_amdgcn_sched_barrier(0);
@@ -1583,14 +1650,19 @@ __global__ __launch_bounds__(WV * 64) void k_gemm_small16(GemmArgs g, int tiles_
 }
 
 // The 16 x 32 small GEMM where the 32 x 32 one would leave fewer than 128
-// blocks for a K of at least 512 (PPDL_SMALL16=0 turns it off; read per call).
+// blocks and K >= 256 (PPDL_SMALL16=0 turns it off, =<k> sets the K bound for
+// A/B runs; read per call).  Same-process graph A/B: K >= 512 (fc2, qpos.1)
+// 37 us per image faster; K >= 256 (also sa.o, ca.op, the box and mask-query
+// heads) 25 us more; K >= 32 7 us slower than K >= 256.
 bool small16_ok(const GemmArgs &g, int amode) {
     const char *e = getenv("PPDL_SMALL16");
     if (e && e[0] == '0') return false;
     const int64_t t32 = (int64_t)((g.M + 31) / 32) * ((g.N + 31) / 32) * g.batch;
     const auto a16 = [](const void *q) { return (((uintptr_t)q) & 15) == 0; };
-    return (amode == 1 || amode == 2) && g.K >= 512 && g.K % kSmallKC == 0 && t32 < 128 && !g.c_trans && !g.bits &&
-           !g.a_add && !g.ln_g && g.lda % 4 == 0 && a16(g.A) &&
+    const int64_t kmin = (e && *e && e[0] != '0') ? atoi(e) : 256;
+    return (amode == 1 || amode == 2) && g.K >= kmin && g.K % kSmallKC == 0 && t32 < 128 && !g.c_trans && !g.bits &&
+           (amode == 1 || !g.ln_g) && (!g.ln_g || g.K == 8 * kSmallKC) && (!g.a_add || g.ln_g) &&
+           (!g.a_add || (a16(g.a_add) && g.a_add_n % 32 == 0)) && g.lda % 4 == 0 && a16(g.A) &&
            (int64_t)g.M * g.lda + g.K < 0x7fffffff && (int64_t)g.K * g.ldb + g.N < 0x7fffffff;
 }
 
@@ -1599,9 +1671,13 @@ hipError_t launch_small16(const GemmArgs &g, int amode, hipStream_t s) {
     const int64_t total = (int64_t)tmn * g.batch;
     if (total <= 0 || total > 0x7fffffff) return hipErrorInvalidValue;
     const dim3 grid((unsigned)total);
-    // 8 waves with the computed A (16 would cap each wave at 128 registers: spills)
-    if (amode == 2) hipLaunchKernelGGL((k_gemm_small16<2, 8>), grid, dim3(512), 0, s, g, tiles_m, tmn);
-    else hipLaunchKernelGGL((k_gemm_small16<1, 16>), grid, dim3(1024), 0, s, g, tiles_m, tmn);
+    // 8 waves with the computed A (16 would cap each wave at 128 registers:
+    // spills); the row norm needs one 32-k chunk per wave
+    if (amode == 2) hipLaunchKernelGGL((k_gemm_small16<2, 8, false, false>), grid, dim3(512), 0, s, g, tiles_m, tmn);
+    else if (g.ln_g && g.a_add)
+        hipLaunchKernelGGL((k_gemm_small16<1, 8, true, true>), grid, dim3(512), 0, s, g, tiles_m, tmn);
+    else if (g.ln_g) hipLaunchKernelGGL((k_gemm_small16<1, 8, true, false>), grid, dim3(512), 0, s, g, tiles_m, tmn);
+    else hipLaunchKernelGGL((k_gemm_small16<1, 16, false, false>), grid, dim3(1024), 0, s, g, tiles_m, tmn);
     return hipGetLastError();
 }
 
@@ -1886,8 +1962,12 @@ bool ln_ok(const GemmArgs &g) {
            (int64_t)g.M * g.lda < 0x7fffffff && (int64_t)g.K * g.ldb < 0x7fffffff;
 }
 
+bool small16_ok(const GemmArgs &g, int amode);
+hipError_t launch_small16(const GemmArgs &g, int amode, hipStream_t s);
+
 hipError_t launch_ln(const GemmArgs &g, hipStream_t s) {
     if (!ln_ok(g)) return hipErrorInvalidValue;
+    if (small16_ok(g, 1)) return launch_small16(g, 1, s);
     const int tiles_m = (g.M + 31) / 32, tiles_n = (g.N + 31) / 32, tmn = tiles_m * tiles_n;
     const dim3 grid((unsigned)tmn);
     const bool pre = g.a_add != nullptr;
@@ -2000,9 +2080,9 @@ std::string gemm_kernel_name(const GemmArgs &g, int64_t ws_bytes, bool im2col) {
     if (im2col && patch_cc(g)) return g.KW == 3 ? "k_conv_patch<3, 2>" : "k_conv_patch<2, 1>";
     if (im2col && direct_ok(g)) return "k_conv_k3s2<" + std::to_string(g.IC) + ">";
     if (im2col && frag_ok(g)) return "k_conv_frag<" + std::to_string(frag_waves(g)) + ">";
-    if (g.a_w4 && small16_ok(g, 2)) return "k_gemm_small16<2, 8>";
+    if (g.a_w4 && small16_ok(g, 2)) return "k_gemm_small16<2, 8, false, false>";
     if (g.a_w4) return "k_gemm_small<2, " + std::to_string(small_waves(g.K, small_tiles(g))) + ", false>";
-    if (g.ln_g) return "k_gemm_small_ln<" + std::to_string(g.K / kSmallKC) + (g.a_add ? ", true>" : ", false>");
+
     const GemmPlan p = gemm_plan(g, ws_bytes, im2col);
     if (!im2col) {
         GemmArgs gv = g;
@@ -2010,7 +2090,9 @@ std::string gemm_kernel_name(const GemmArgs &g, int64_t ws_bytes, bool im2col) {
         const int lc = gemm_lt_pick(gv, 8 * cus_per_xcd(), lt_wanted(gv, p));
         if (lc >= 0) return gemm_lt_name(lc);
     }
-    if (p.cfg == kCfgSmall && g.a_rowmajor && small16_ok(g, 1)) return "k_gemm_small16<1, 16>";
+    if (g.a_rowmajor && (g.ln_g || p.cfg == kCfgSmall) && small16_ok(g, 1))
+        return std::string("k_gemm_small16<1, ") + (g.ln_g ? "8, true, " : "16, false, ") + (g.a_add ? "true>" : "false>");  // a_add only with ln_g
+    if (g.ln_g) return "k_gemm_small_ln<" + std::to_string(g.K / kSmallKC) + (g.a_add ? ", true>" : ", false>");
     if (p.cfg == kCfgSmall)
         return std::string("k_gemm_small<") + (g.a_rowmajor ? "1, " : "0, ") +
                std::to_string(small_waves(g.K, small_tiles(g))) + (g.a_add && g.a_rowmajor ? ", true>" : ", false>");
