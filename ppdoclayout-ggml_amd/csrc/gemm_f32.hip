@@ -1649,19 +1649,22 @@ __global__ __launch_bounds__(WV * 64) void k_gemm_small16(GemmArgs g, int tiles_
     }
 }
 
-// The 16 x 32 small GEMM where the 32 x 32 one would leave fewer than 128
-// blocks and K >= 256 (PPDL_SMALL16=0 turns it off, =<k> sets the K bound for
-// A/B runs; read per call).  Same-process graph A/B: K >= 512 (fc2, qpos.1)
-// 37 us per image faster; K >= 256 (also sa.o, ca.op, the box and mask-query
-// heads) 25 us more; K >= 32 7 us slower than K >= 256.
+// The 16 x 32 small GEMM where the 32 x 32 one would leave fewer than 400
+// blocks and K >= 256 (PPDL_SMALL16=0 turns it off, =<k> sets the K bound,
+// PPDL_SMALL16_T the block bound, for A/B runs; read per call).  Same-process
+// graph A/B: K >= 512 (fc2, qpos.1) 37 us per image faster; K >= 256 (also
+// sa.o, ca.op, the box and mask-query heads) 25 us more; K >= 32 7 us slower
+// than K >= 256; a bound of 400 instead of 128 blocks (adds sa.qkv, fc1) 3 us.
 bool small16_ok(const GemmArgs &g, int amode) {
     const char *e = getenv("PPDL_SMALL16");
     if (e && e[0] == '0') return false;
     const int64_t t32 = (int64_t)((g.M + 31) / 32) * ((g.N + 31) / 32) * g.batch;
     const auto a16 = [](const void *q) { return (((uintptr_t)q) & 15) == 0; };
     const int64_t kmin = (e && *e && e[0] != '0') ? atoi(e) : 256;
-    return (amode == 1 || amode == 2) && g.K >= kmin && g.K % kSmallKC == 0 && t32 < 128 && !g.c_trans && !g.bits &&
-           (amode == 1 || !g.ln_g) && (!g.ln_g || g.K == 8 * kSmallKC) && (!g.a_add || g.ln_g) &&
+    const char *et = getenv("PPDL_SMALL16_T");
+    const int64_t tmax = (et && *et) ? atoi(et) : 400;
+    return (amode == 1 || amode == 2) && g.K >= kmin && g.K % kSmallKC == 0 && t32 < tmax && !g.c_trans && !g.bits &&
+           (amode == 1 || !g.ln_g) && (!g.ln_g || g.K == 8 * kSmallKC) &&
            (!g.a_add || (a16(g.a_add) && g.a_add_n % 32 == 0)) && g.lda % 4 == 0 && a16(g.A) &&
            (int64_t)g.M * g.lda + g.K < 0x7fffffff && (int64_t)g.K * g.ldb + g.N < 0x7fffffff;
 }
@@ -1677,6 +1680,7 @@ hipError_t launch_small16(const GemmArgs &g, int amode, hipStream_t s) {
     else if (g.ln_g && g.a_add)
         hipLaunchKernelGGL((k_gemm_small16<1, 8, true, true>), grid, dim3(512), 0, s, g, tiles_m, tmn);
     else if (g.ln_g) hipLaunchKernelGGL((k_gemm_small16<1, 8, true, false>), grid, dim3(512), 0, s, g, tiles_m, tmn);
+    else if (g.a_add) hipLaunchKernelGGL((k_gemm_small16<1, 16, false, true>), grid, dim3(1024), 0, s, g, tiles_m, tmn);
     else hipLaunchKernelGGL((k_gemm_small16<1, 16, false, false>), grid, dim3(1024), 0, s, g, tiles_m, tmn);
     return hipGetLastError();
 }
@@ -2091,7 +2095,7 @@ std::string gemm_kernel_name(const GemmArgs &g, int64_t ws_bytes, bool im2col) {
         if (lc >= 0) return gemm_lt_name(lc);
     }
     if (g.a_rowmajor && (g.ln_g || p.cfg == kCfgSmall) && small16_ok(g, 1))
-        return std::string("k_gemm_small16<1, ") + (g.ln_g ? "8, true, " : "16, false, ") + (g.a_add ? "true>" : "false>");  // a_add only with ln_g
+        return std::string("k_gemm_small16<1, ") + (g.ln_g ? "8, true, " : "16, false, ") + (g.a_add ? "true>" : "false>");
     if (g.ln_g) return "k_gemm_small_ln<" + std::to_string(g.K / kSmallKC) + (g.a_add ? ", true>" : ", false>");
     if (p.cfg == kCfgSmall)
         return std::string("k_gemm_small<") + (g.a_rowmajor ? "1, " : "0, ") +
