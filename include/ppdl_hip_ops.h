@@ -109,6 +109,9 @@ PPDL_HIP_API int ppdl_hip_supports(const int32_t op_params[16], const ppdl_tview
  *               dst ne(T,IC,36): dst[p][ic][t] = (Bt d B)[p] of the 6x6 patch.
  *  11 WG4_OUTPUT src: yt ne(T,OC,36), bias ne(OC); params[14] = act,
  *               [15] = TW; dst ne(W,H,OC) with T = ceil(W/4)*ceil(H/4).
+ *               Optional src[2]: a contiguous map of dst's shape added after
+ *               the activation (no counterpart in the reference's op, which
+ *               takes two sources; the CSP layers end with it).
  *  12 WG4_MADD  src: dt ne(T,IC,36), wg4 ne(OC,IC,36); dst yt ne(T,OC,36):
  *               yt[p][oc][t] = sum_ic dt[p][ic][t] * wg4[p][ic][oc].
  *  1  MASKBOX   src: mask logits ne(40000,NQ); dst ne(4,NQ).

@@ -138,6 +138,8 @@ class Net {
 
     bool load(const std::string &path, std::string *err);
     bool fold_repvgg(GgufFile &g, const std::string &bp, std::string *err);
+    bool concat_conv1x1(GgufFile &g, const std::vector<std::string> &parts, const std::string &name,
+                        std::string *err);
     bool concat_linears(GgufFile &g, const std::vector<std::string> &parts, const std::string &name,
                         std::string *err);
     bool build(bool dumps, std::string *err);
@@ -383,9 +385,11 @@ bool Net::load(const std::string &path, std::string *err) {
         for (int i = 0; i < 6; i++) vp.push_back("dec" + std::to_string(i) + ".ca.vp");
         if (!concat_linears(g, vp, "dec.ca.vp", err)) return false;
     }
-    for (const std::string blk : {"fpn0", "fpn1", "pan0", "pan1"})
+    for (const std::string blk : {"fpn0", "fpn1", "pan0", "pan1"}) {
         for (int i = 0; i < 3; i++)
             if (!fold_repvgg(g, blk + ".bn" + std::to_string(i), err)) return false;
+        if (!concat_conv1x1(g, {blk + ".c1", blk + ".c2"}, blk + ".c12", err)) return false;
+    }
     if (oom_) {
         *err = "device allocation failed";
         return false;
@@ -426,6 +430,42 @@ bool Net::fold_repvgg(GgufFile &g, const std::string &bp, std::string *err) {
     w_[bp + ".rep.wg4"] = upload(wg4);
     w_[bp + ".rep.bias"] = upload(b1);
     ne_[bp + ".rep.weight"] = t1.ne;
+    return true;
+}
+
+// 1x1 convs `parts` over the same input (weights ne(1, 1, IC, OC_i)) stored
+// as one conv `name` whose output channels are the parts' in order (.wr,
+// .bias, shape): one GEMM instead of one per part, the same sums.  Skipped
+// (no entry) when a part is absent or not a 1x1 conv over IC.
+bool Net::concat_conv1x1(GgufFile &g, const std::vector<std::string> &parts, const std::string &name,
+                         std::string *err) {
+    int64_t IC = -1, total = 0;
+    for (const auto &p : parts) {
+        if (!g.index.count(p + ".weight") || !g.index.count(p + ".bias")) return true;
+        const auto &t = g.tensors[g.index[p + ".weight"]];
+        if (t.ne.size() != 4 || t.ne[0] != 1 || t.ne[1] != 1 || (IC >= 0 && t.ne[2] != IC)) return true;
+        if (g.tensors[g.index[p + ".bias"]].nelem() != t.ne[3]) return true;
+        IC = t.ne[2];
+        total += t.ne[3];
+    }
+    std::vector<float> w((size_t)(IC * total)), b((size_t)total);
+    int64_t o0 = 0;
+    for (const auto &p : parts) {
+        const auto &t = g.tensors[g.index[p + ".weight"]];
+        // [oc][ic] rows of the part follow the previous parts' rows
+        if (!gguf_read_f32(g, t, w.data() + o0 * IC, err) ||
+            !gguf_read_f32(g, g.tensors[g.index[p + ".bias"]], b.data() + o0, err))
+            return false;
+        o0 += t.ne[3];
+    }
+    std::vector<float> wr((size_t)(IC * total));
+    if (ppdl_hip_repack_conv(w.data(), (int)total, (int)IC, 1, wr.data(), nullptr) != PPDL_OK) {
+        *err = "repack failed: " + name;
+        return false;
+    }
+    w_[name + ".wr"] = upload(wr);
+    w_[name + ".bias"] = upload(b);
+    ne_[name + ".weight"] = {1, 1, IC, total};
     return true;
 }
 
@@ -519,8 +559,9 @@ Img Net::conv(const Img &x, const std::string &name, int s, int p, int act, floa
             n.bytes = 4.0 * ((double)x.C * x.H * x.W + 36.0 * x.C * OC + (double)OC * OH * OW);
             n.kern = wg4_conv_kernel_name(x.C, x.H, x.W, OC);
         }
-    } else if (K == 3 && s == 1 && p == 1 && pad_end == 0 && add_mode == 0) {
-        // Winograd F(4,3): pad fused into op 15, madd (op 12), output + bias + act (op 11) (:425-463)
+    } else if (K == 3 && s == 1 && p == 1 && pad_end == 0 && (add_mode == 0 || add_mode == 2)) {
+        // Winograd F(4,3): pad fused into op 15, madd (op 12), output + bias + act (op 11) (:425-463);
+        // add_mode 2 adds `add` after the activation in op 11
         const int TW = (OW + 3) / 4, TH = (OH + 3) / 4, T = TW * TH;
         // plane rows padded to a multiple of 4 tiles: the madd GEMM then reads
         // whole float4s (and may copy them straight to LDS) on every tile
@@ -557,8 +598,8 @@ Img Net::conv(const Img &x, const std::string &name, int s, int p, int act, floa
         }
         node(name + ".wg_out", 1, [=](hipStream_t st) {
             ppdl_tview d = view(y);
-            ppdl_tview sv[2] = {planes(sc->yt, T, OC, ldt), view(b, {OC})};
-            return ppdl_hip_run(p_out.data(), &d, sv, 2, st);
+            ppdl_tview sv[3] = {planes(sc->yt, T, OC, ldt), view(b, {OC}), view(add, {OW, OH, OC})};
+            return ppdl_hip_run(p_out.data(), &d, sv, add_mode ? 3 : 2, st);
         });
     } else {
         // k2, k3 s2: implicit-im2col GEMM + bias + act (op 16), replacing
@@ -693,6 +734,23 @@ Img Net::csp(const Img &x, const std::string &pfx, float *out) {
     // PPDL_REPVGG=0 keeps the two-conv form of the RepVGG blocks (A/B runs)
     const char *e = getenv("PPDL_REPVGG");
     const bool fold = !(e && e[0] == '0');
+    // c1 and c2 read the same input: one GEMM into [a | t2] (2C planes);
+    // the last folded block adds t2 = silu(c2(x)) after its activation in
+    // its output transform (PPDL_CSP_MERGE=0: two GEMMs, for A/B runs)
+    const char *em = getenv("PPDL_CSP_MERGE");
+    bool merge = fold && !(em && em[0] == '0') && w_.count(pfx + ".c12.wr");
+    for (int i = 0; merge && i < 3; i++) merge = w_.count(pfx + ".bn" + std::to_string(i) + ".rep.wg4") > 0;
+    if (merge) {
+        const Img at = conv(x, pfx + ".c12", 1, 0, kActSilu);
+        const int C = at.C / 2;
+        Img a{at.d, C, at.H, at.W};
+        const float *t2 = at.d + (int64_t)C * at.H * at.W;
+        for (int i = 0; i < 3; i++) {
+            const std::string bp = pfx + ".bn" + std::to_string(i);
+            a = i < 2 ? conv(a, bp + ".rep", 1, 1, kActSilu) : conv(a, bp + ".rep", 1, 1, kActSilu, out, 0, t2, 2);
+        }
+        return a;
+    }
     Img a = conv(x, pfx + ".c1", 1, 0, kActSilu);
     for (int i = 0; i < 3; i++) {
         const std::string bp = pfx + ".bn" + std::to_string(i);

@@ -144,7 +144,8 @@ std::string gemm_lt_name(int cfg);
 // dt / yt planes: [36][C][ldt] with the T = TW*TH tiles first in each row
 hipError_t wg4_input(const float *x, float *dt, int IW, int IH, int IC, int TW, int TH, int pad, int ldt,
                      hipStream_t s);
-hipError_t wg4_output(const float *yt, const float *bias, float *out, int TW, int TH, int OC,
+// add (optional, out's shape): added after the activation
+hipError_t wg4_output(const float *yt, const float *bias, const float *add, float *out, int TW, int TH, int OC,
                       int OW, int OH, int act, int ldt, hipStream_t s);
 // the whole k3 s1 p1 conv in one kernel (op 17): x [IC][H][W], wg4
 // [36][IC][OC], out [OC][H][W] = act(conv + bias)

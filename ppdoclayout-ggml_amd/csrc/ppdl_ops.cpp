@@ -193,6 +193,10 @@ int check_op(const int32_t *p, const ppdl_tview *dst, const ppdl_tview *src, int
             const int64_t TW = (OW + 3) / 4, TH = (OH + 3) / 4;
             if (dst->ne[3] != 1 || !planes_f32(&src[0], TW * TH, OC)) return PPDL_EINVAL;
             if (p[15] != TW || nelem(&src[1]) != OC || p[14] < 0 || p[14] > 2) return PPDL_EINVAL;
+            // optional third source: a map of dst's shape added after the activation
+            if (nsrc >= 3 && (!contig_f32(&src[2]) || src[2].ne[0] != OW || src[2].ne[1] != OH ||
+                              src[2].ne[2] != OC || src[2].ne[3] != 1))
+                return PPDL_EINVAL;
             return PPDL_OK;
         }
         case PPDL_OP_CONV_IM2COL: {
@@ -405,6 +409,7 @@ int ppdl::run_node(const int32_t *p, const ppdl_tview *dst, const ppdl_tview *sr
         case PPDL_OP_WG4_OUTPUT: {
             const int OW = (int)dst->ne[0], OH = (int)dst->ne[1], OC = (int)dst->ne[2];
             return status_of(wg4_output((const float *)src[0].data, (const float *)src[1].data,
+                                        nsrc >= 3 ? (const float *)src[2].data : nullptr,
                                         (float *)dst->data, (OW + 3) / 4, (OH + 3) / 4, OC, OW, OH,
                                         p[14], (int)(src[0].nb[1] / 4), s));
         }

@@ -134,8 +134,10 @@ __global__ __launch_bounds__(kThreads) void k_wg4_input(const float *__restrict_
     for (int p = 0; p < 36; p++) o[p * pstride] = v[p];
 }
 
+// add (optional, out's shape): a map added after the activation
 __global__ __launch_bounds__(kThreads) void k_wg4_output(const float *__restrict__ yt,
                                                          const float *__restrict__ bias,
+                                                         const float *__restrict__ add,
                                                          float *__restrict__ out, int TW, int TH,
                                                          int OC, int OW, int OH, int act, int ldt) {
     const int T = TW * TH;
@@ -160,19 +162,26 @@ __global__ __launch_bounds__(kThreads) void k_wg4_output(const float *__restrict
         for (int j = 0; j < 4; j++) Y[i][j] = act_f(Y[i][j] + b, act);
 
     float *__restrict__ oplane = out + (int64_t)oc * OH * OW;
+    const float *__restrict__ aplane = add ? add + (int64_t)oc * OH * OW : nullptr;
     const int px = 4 * tx;
-    const bool vec = ((OW & 3) == 0) && ((((uintptr_t)out) & 15) == 0) && (px + 3 < OW);
+    const bool vec = ((OW & 3) == 0) && ((((uintptr_t)out | (uintptr_t)add) & 15) == 0) && (px + 3 < OW);
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         const int py = 4 * ty + i;
         if (py < OH) {
             float *row = oplane + (int64_t)py * OW + px;
+            const float *arow = aplane ? aplane + (int64_t)py * OW + px : nullptr;
             if (vec) {
-                *reinterpret_cast<float4 *>(row) = make_float4(Y[i][0], Y[i][1], Y[i][2], Y[i][3]);
+                float4 v = make_float4(Y[i][0], Y[i][1], Y[i][2], Y[i][3]);
+                if (arow) {
+                    const float4 a = *reinterpret_cast<const float4 *>(arow);
+                    v.x += a.x, v.y += a.y, v.z += a.z, v.w += a.w;
+                }
+                *reinterpret_cast<float4 *>(row) = v;
             } else {
 #pragma unroll
                 for (int j = 0; j < 4; j++)
-                    if (px + j < OW) row[j] = Y[i][j];
+                    if (px + j < OW) row[j] = arow ? Y[i][j] + arow[j] : Y[i][j];
             }
         }
     }
@@ -505,11 +514,11 @@ hipError_t wg4_input(const float *x, float *dt, int IW, int IH, int IC, int TW, 
     return hipGetLastError();
 }
 
-hipError_t wg4_output(const float *yt, const float *bias, float *out, int TW, int TH, int OC,
+hipError_t wg4_output(const float *yt, const float *bias, const float *add, float *out, int TW, int TH, int OC,
                       int OW, int OH, int act, int ldt, hipStream_t s) {
     const int64_t n = (int64_t)TW * TH * OC;
     const unsigned blocks = (unsigned)((n + kThreads - 1) / kThreads);
-    hipLaunchKernelGGL(k_wg4_output, dim3(blocks), dim3(kThreads), 0, s, yt, bias, out, TW, TH, OC,
+    hipLaunchKernelGGL(k_wg4_output, dim3(blocks), dim3(kThreads), 0, s, yt, bias, add, out, TW, TH, OC,
                        OW, OH, act, ldt);
     return hipGetLastError();
 }
