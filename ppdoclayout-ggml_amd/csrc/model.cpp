@@ -207,8 +207,39 @@ class Net {
 
     // ---- node emission ----
     void node(const std::string &name, int kernels, std::function<int(hipStream_t)> fn) {
+        if (pend_.on) flush_pending();
         nodes_.push_back({name, kernels, std::move(fn)});
         nodes_.back().lane = lane_;
+    }
+    // A Winograd conv's output transform is held back until the next node:
+    // when that is the input transform of a Winograd conv on exactly this
+    // output, both become one chained node (wg4_chain); before any other
+    // node it is emitted as op 11.  Opt-in (PPDL_WG_CHAIN=1): the 13 chains
+    // of the network (stage 2's layer chain, the RepVGG chains of the four
+    // CSP layers) remove 13 launches, yet the graph replayed 6-10 us slower
+    // (same-process A/B, bands of 4 and 8 tile rows): the recomputed halo
+    // rows and the kernel's two dependent phases cost what the launch saved.
+    struct Scratch;
+    struct PendOut {
+        bool on = false;
+        std::string name;
+        Img y;
+        const float *bias = nullptr, *add = nullptr;
+        int act = 0, add_mode = 0, ldt = 0, TW = 0, TH = 0;
+        Scratch *sc = nullptr;
+        std::vector<int32_t> p_out;
+    };
+    PendOut pend_;
+    void flush_pending() {
+        const PendOut pp = pend_;
+        pend_.on = false;
+        Scratch *sc = pp.sc;
+        const int T = pp.TW * pp.TH, OC = pp.y.C, OW = pp.y.W, OH = pp.y.H;
+        node(pp.name + ".wg_out", 1, [=](hipStream_t st) {
+            ppdl_tview d = view(pp.y);
+            ppdl_tview sv[3] = {planes(sc->yt, T, OC, pp.ldt), view(pp.bias, {OC}), view(pp.add, {OW, OH, OC})};
+            return ppdl_hip_run(pp.p_out.data(), &d, sv, pp.add_mode ? 3 : 2, st);
+        });
     }
     // Independent branches: fork(l) makes lane l wait for everything emitted
     // so far on the main lane and directs the following nodes to lane l;
@@ -227,6 +258,7 @@ class Net {
         lane_ = 0;
     }
     void sync_node(const char *nm, int kind, int l) {
+        if (pend_.on) flush_pending();
         hipEvent_t e = nullptr;
         if (hipEventCreateWithFlags(&e, hipEventDisableTiming) != hipSuccess) {
             if (bad_node_.empty()) bad_node_ = nm;
@@ -576,15 +608,27 @@ Img Net::conv(const Img &x, const std::string &name, int s, int p, int act, floa
         const float *wg4 = W(name + ".wg4");
         const auto p_in = op_params(PPDL_OP_WG4_INPUT_PAD, T, TH), p_md = op_params(PPDL_OP_WG4_MADD, 0, 0),
                    p_out = op_params(PPDL_OP_WG4_OUTPUT, act, TW);
+        const char *ech = getenv("PPDL_WG_CHAIN");
+        const bool chaining = ech && ech[0] == '1';
         const ppdl_tview qd = planes(kShapeOnly, T, OC, ldt);
         const ppdl_tview qs[2] = {planes(kShapeOnly, T, x.C, ldt), view(wg4, {OC, x.C, 36})};
         const int64_t wsb = ppdl_hip_workspace_bytes(p_md.data(), &qd, qs, 2);
         if (wsb < 0 && bad_node_.empty()) bad_node_ = name;
         sc->ws_need = std::max(sc->ws_need, wsb);
-        node(name + ".wg_in", 1, [=](hipStream_t st) {
-            ppdl_tview d = planes(sc->dt, T, xi.C, ldt), sx = view(xi);
-            return ppdl_hip_run(p_in.data(), &d, &sx, 1, st);
-        });
+        if (pend_.on && pend_.sc == sc && pend_.add_mode == 0 && pend_.y.d == x.d && pend_.y.C == x.C &&
+            pend_.y.H == x.H && pend_.y.W == x.W && !x.ld && pend_.ldt == ldt && wg4_chain_fits(x.W)) {
+            // the previous conv's output transform and this one's input transform
+            const PendOut pp = pend_;
+            pend_.on = false;
+            node(pp.name + ".wg_chain", 1, [=](hipStream_t st) {
+                return ok(wg4_chain(sc->yt, pp.bias, pp.y.d, sc->dt, xi.C, xi.W, xi.H, pp.act, ldt, ldt, st));
+            });
+        } else {
+            node(name + ".wg_in", 1, [=](hipStream_t st) {
+                ppdl_tview d = planes(sc->dt, T, xi.C, ldt), sx = view(xi);
+                return ppdl_hip_run(p_in.data(), &d, &sx, 1, st);
+            });
+        }
         node(name + ".wg_madd", wsb > 0 ? 2 : 1, [=](hipStream_t st) {
             ppdl_tview d = planes(sc->yt, T, OC, ldt);
             std::vector<ppdl_tview> sv = {planes(sc->dt, T, xi.C, ldt), view(wg4, {OC, xi.C, 36})};
@@ -596,11 +640,21 @@ Img Net::conv(const Img &x, const std::string &name, int s, int p, int act, floa
             bool im2col;
             if (gemm_args_of(p_md.data(), &qd, qs, &g, &im2col)) gemm_meta(1, g, wsb, im2col);
         }
-        node(name + ".wg_out", 1, [=](hipStream_t st) {
-            ppdl_tview d = view(y);
-            ppdl_tview sv[3] = {planes(sc->yt, T, OC, ldt), view(b, {OC}), view(add, {OW, OH, OC})};
-            return ppdl_hip_run(p_out.data(), &d, sv, add_mode ? 3 : 2, st);
-        });
+        PendOut po;
+        po.on = true;
+        po.name = name;
+        po.y = y;
+        po.bias = b;
+        po.add = add;
+        po.act = act;
+        po.add_mode = add_mode;
+        po.ldt = ldt;
+        po.TW = TW;
+        po.TH = TH;
+        po.sc = sc;
+        po.p_out = p_out;
+        pend_ = po;
+        if (!chaining) flush_pending();
     } else {
         // k2, k3 s2: implicit-im2col GEMM + bias + act (op 16), replacing
         // im2col + mul_mat + permute/cont + add + act (:535-542)
@@ -1020,6 +1074,7 @@ bool Net::build(bool dumps, std::string *err) {
     order_ = alloc((int64_t)NQ * NQ);
     node("order", 1, [=](hipStream_t st) { return ok(order_logits(gp.d, order_, NQ, 64, 1.0f / 8.0f, st)); });
 
+    if (pend_.on) flush_pending();
     if (!missing_.empty()) {
         *err = "missing tensor: " + missing_;
         return false;

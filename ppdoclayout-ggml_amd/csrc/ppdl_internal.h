@@ -144,6 +144,11 @@ std::string gemm_lt_name(int cfg);
 // dt / yt planes: [36][C][ldt] with the T = TW*TH tiles first in each row
 hipError_t wg4_input(const float *x, float *dt, int IW, int IH, int IC, int TW, int TH, int pad, int ldt,
                      hipStream_t s);
+// conv i's output transform (+ bias + act, y stored [C][OH][OW]) and conv
+// i+1's input transform (pad 1) of y into dt [36][C][ldt_in], one launch
+hipError_t wg4_chain(const float *yt, const float *bias, float *y, float *dt, int C, int OW, int OH, int act,
+                     int ldt_out, int ldt_in, hipStream_t s);
+bool wg4_chain_fits(int OW);  // the band of a map OW wide fits the kernel's LDS
 // add (optional, out's shape): added after the activation
 hipError_t wg4_output(const float *yt, const float *bias, const float *add, float *out, int TW, int TH, int OC,
                       int OW, int OH, int act, int ldt, hipStream_t s);

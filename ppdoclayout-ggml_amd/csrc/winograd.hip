@@ -23,6 +23,7 @@ namespace ppdl {
 namespace {
 
 constexpr int kThreads = 256;
+constexpr int kChainRows = 8;  // tile rows per band of the chained transforms
 
 // v = Bt d Bt^T of one 6x6 patch, plane p = u*6 + v: a fixed chain of fmaf
 // over the nonzero entries in ascending index order (the oracle repeats it)
@@ -184,6 +185,91 @@ __global__ __launch_bounds__(kThreads) void k_wg4_output(const float *__restrict
                     if (px + j < OW) row[j] = arow ? Y[i][j] + arow[j] : Y[i][j];
             }
         }
+    }
+}
+
+
+// ---------------------------------------------------------------------------
+// Chained transforms: the output transform of conv i (+ bias + act, its map
+// y stored) and the input transform (pad 1) of conv i+1 on that map in one
+// kernel, so y is not read back from memory and one launch disappears.
+// A block owns a band of RB tile rows x all TW tile columns for CB channels:
+//   1. output tiles of rows ty0 - 1 .. ty0 + RB (one halo row above and
+//      below, recomputed by the neighbouring bands too) into an LDS image of
+//      the band with a one-pixel frame; pixels outside the map are zero (the
+//      next conv's padding); the band's own rows are also stored to y;
+//   2. input transforms of the band's tiles from the LDS image, stored to
+//      dt [36][C][ldt_in] like op 15.
+// LDS row k holds map row 4 (ty0 - 1) + k, LDS column k map column k - 1.
+template <int CB>
+__global__ __launch_bounds__(kThreads) void k_wg4_chain(const float *__restrict__ yt, const float *__restrict__ bias,
+                                                        float *__restrict__ y, float *__restrict__ dt, int TW, int TH,
+                                                        int C, int OW, int OH, int act, int ldt_out, int ldt_in) {
+    constexpr int RB = kChainRows;
+    extern __shared__ float band[];  // [CB][LH][LW]
+    const int LW = 4 * TW + 2, LH = 4 * (RB + 2);
+    const int nb = (TH + RB - 1) / RB;
+    const int ty0 = (int)(blockIdx.x % nb) * RB, c0 = (int)(blockIdx.x / nb) * CB;
+    const int64_t pout = (int64_t)C * ldt_out, pin = (int64_t)C * ldt_in;
+
+    // frame columns (map columns -1 and 4 TW): zero
+    for (int i = threadIdx.x; i < CB * LH; i += kThreads) {
+        band[i * LW] = 0.0f;
+        band[i * LW + LW - 1] = 0.0f;
+    }
+    const int n1 = CB * (RB + 2) * TW;
+    for (int task = threadIdx.x; task < n1; task += kThreads) {
+        const int cc = task / ((RB + 2) * TW), r = task - cc * ((RB + 2) * TW);
+        const int tyl = r / TW, tx = r - tyl * TW;
+        const int ty = ty0 - 1 + tyl, c = c0 + cc;
+        const bool live = ty >= 0 && ty < TH && c < C;
+        float Y[4][4];
+        if (live) {
+            const float *src = yt + (int64_t)c * ldt_out + ty * TW + tx;
+            float m[6][6];
+#pragma unroll
+            for (int p = 0; p < 36; p++) m[p / 6][p % 6] = src[p * pout];
+            output_tile(m, Y);
+            const float b = bias[c];
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) Y[i][j] = act_f(Y[i][j] + b, act);
+        }
+        float *lrow = band + ((int64_t)cc * LH + 4 * tyl) * LW + 1 + 4 * tx;
+        const bool own = live && tyl >= 1 && tyl <= RB;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int py = 4 * ty + i;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int px = 4 * tx + j;
+                const bool in = live && py < OH && px < OW;
+                lrow[i * LW + j] = in ? Y[i][j] : 0.0f;
+                if (own && in) y[((int64_t)c * OH + py) * OW + px] = Y[i][j];
+            }
+        }
+    }
+    __syncthreads();
+    const int n2 = CB * RB * TW;
+    for (int task = threadIdx.x; task < n2; task += kThreads) {
+        const int cc = task / (RB * TW), r = task - cc * (RB * TW);
+        const int tyl = r / TW, tx = r - tyl * TW;
+        const int ty = ty0 + tyl, c = c0 + cc;
+        if (ty >= TH || c >= C) continue;
+        // patch rows: map rows 4 ty - 1 + a = LDS rows 4 tyl + 3 + a; columns
+        // 4 tx - 1 + b = LDS columns 4 tx + b
+        const float *l = band + ((int64_t)cc * LH + 4 * tyl + 3) * LW + 4 * tx;
+        float d[6][6];
+#pragma unroll
+        for (int a = 0; a < 6; a++)
+#pragma unroll
+            for (int b = 0; b < 6; b++) d[a][b] = l[a * LW + b];
+        float v[36];
+        input_tile(d, v);
+        float *o = dt + (int64_t)c * ldt_in + ty * TW + tx;
+#pragma unroll
+        for (int p = 0; p < 36; p++) o[p * pin] = v[p];
     }
 }
 
@@ -511,6 +597,31 @@ hipError_t wg4_input(const float *x, float *dt, int IW, int IH, int IC, int TW, 
         hipLaunchKernelGGL(k_wg4_input<1>, dim3(blocks), dim3(kThreads), 0, s, x, dt, IW, IH, IC, TW, TH, ldt, vec);
     else
         hipLaunchKernelGGL(k_wg4_input<0>, dim3(blocks), dim3(kThreads), 0, s, x, dt, IW, IH, IC, TW, TH, ldt, 0);
+    return hipGetLastError();
+}
+
+bool wg4_chain_fits(int OW) {
+    return (size_t)2 * 4 * (kChainRows + 2) * (4 * ((OW + 3) / 4) + 2) * sizeof(float) <= 64 * 1024;
+}
+
+hipError_t wg4_chain(const float *yt, const float *bias, float *y, float *dt, int C, int OW, int OH, int act,
+                     int ldt_out, int ldt_in, hipStream_t s) {
+    const int TW = (OW + 3) / 4, TH = (OH + 3) / 4, T = TW * TH;
+    const int nb = (TH + kChainRows - 1) / kChainRows;
+    if (C < 1 || OW < 1 || OH < 1 || ldt_out < T || ldt_in < T) return hipErrorInvalidValue;
+    // 4 channels per block when that still gives 256 blocks and fits 64 KB
+    // of LDS, else 2
+    const size_t per_c = (size_t)4 * (kChainRows + 2) * (4 * TW + 2) * sizeof(float);
+    const int cb = ((int64_t)nb * ((C + 3) / 4) >= 256 && 4 * per_c <= 64 * 1024) ? 4 : 2;
+    const size_t lds = cb * per_c;
+    if (lds > 64 * 1024) return hipErrorInvalidValue;
+    const unsigned blocks = (unsigned)(nb * ((C + cb - 1) / cb));
+    if (cb == 4)
+        hipLaunchKernelGGL(k_wg4_chain<4>, dim3(blocks), dim3(kThreads), lds, s, yt, bias, y, dt, TW, TH, C, OW, OH,
+                           act, ldt_out, ldt_in);
+    else
+        hipLaunchKernelGGL(k_wg4_chain<2>, dim3(blocks), dim3(kThreads), lds, s, yt, bias, y, dt, TW, TH, C, OW, OH,
+                           act, ldt_out, ldt_in);
     return hipGetLastError();
 }
 

@@ -247,3 +247,33 @@ def test_cli_matches_api(gpu, model, image, tmp_path):
     assert r.returncode == 0, r.stderr
     for d in ("b0", "b1"):
         assert np.array_equal(np.fromfile(tmp_path / d / "out0.bin", np.float32).reshape(300, 7), dets)
+
+
+def test_chained_winograd_transforms_match(gpu, model, image, monkeypatch):
+    """The opt-in chained Winograd transforms (PPDL_WG_CHAIN=1: one kernel
+    writes a conv's output and the next conv's transformed input) against
+    the default graph on the same page: fewer launches, raw outputs within
+    the network tolerance, the same top-300 selection."""
+    import ppdoclayout as P
+
+    _, raw, _, _, _ = gpu
+    monkeypatch.setenv("PPDL_WG_CHAIN", "1")
+    ctx = P.PPDocLayout(model[0], P.BACKEND_HIP)
+    try:
+        n_default, n_chain = gpu[0].graph_nodes(), ctx.graph_nodes()
+        say("graph kernel launches: default", n_default, "chained", n_chain)
+        assert n_chain < n_default
+        ctx.compute(image)
+        topk = ctx.raw(P.RAW_TOPK)
+        assert np.array_equal(np.sort(topk), np.sort(raw["topk"]))
+        pos = {int(t): i for i, t in enumerate(topk)}
+        p = np.array([pos[int(t)] for t in raw["topk"]])  # swaps of tied scores only
+        for k, w in (("logits", P.RAW_LOGITS), ("boxes", P.RAW_BOXES), ("order", P.RAW_ORDER),
+                     ("masks", P.RAW_MASKS)):
+            got = ctx.raw(w)
+            got = got[p][:, p] if k == "order" else got[p]
+            err = normwise(got, raw[k])
+            say("%-10s chained vs default normwise %.3g" % (k, err))
+            assert err <= TOL_OUTPUT, (k, err)
+    finally:
+        ctx.close()
