@@ -961,9 +961,28 @@ bool Net::build(bool dumps, std::string *err) {
     fork(2);
     const Seq vcat = lin(source, "dec.ca.vp", kActNone);
     main_lane();
-    Seq memory{alloc((int64_t)NTOK * kDM), NTOK, kDM, kDM};
-    node("memory", 1, [=](hipStream_t st) { return ok(mul_rows(source.d, valid_, memory.d, NTOK, kDM, st)); });
-    Seq om = ln(lin(memory, "enc_out.l", kActNone), nullptr, "enc_out.ln");
+    // memory = source * valid (:797), consumed only by enc_out.l.  valid is 0
+    // or 1 per token, so enc_out.l(memory) equals enc_out.l(source) on valid
+    // rows and the bias row on masked ones (a zero row through the GEMM: every
+    // product is a zero, as long as source is finite): the GEMM runs on
+    // source and the LayerNorm takes the bias for masked rows.  PPDL_MEMORY=1
+    // keeps the multiply as its own node.
+    const char *emem = getenv("PPDL_MEMORY");
+    Seq om;
+    if (emem && emem[0] == '1') {
+        Seq memory{alloc((int64_t)NTOK * kDM), NTOK, kDM, kDM};
+        node("memory", 1, [=](hipStream_t st) { return ok(mul_rows(source.d, valid_, memory.d, NTOK, kDM, st)); });
+        om = ln(lin(memory, "enc_out.l", kActNone), nullptr, "enc_out.ln");
+    } else {
+        const Seq eo = lin(source, "enc_out.l", kActNone);
+        om = Seq{alloc((int64_t)NTOK * kDM), NTOK, kDM, kDM};
+        const float *gm = W("enc_out.ln.weight"), *bt = W("enc_out.ln.bias"), *fill = W("enc_out.l.bias");
+        const float *mask = valid_;
+        const Seq o = om;
+        node("enc_out.ln", 1, [=](hipStream_t st) {
+            return ok(layernorm(eo.d, nullptr, gm, bt, o.d, NTOK, 0, st, mask, fill));
+        });
+    }
     Seq ecls = lin(om, "score_head", kActNone);  // (13125, 25)
     topk_ = (int32_t *)alloc(NQ);
     tagged("topk300", PPDL_OP_TOPK, 0, 0, view(topk_, {NQ}, PPDL_TYPE_I32), {view(ecls.d, {NC, NTOK})});

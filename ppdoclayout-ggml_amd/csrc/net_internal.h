@@ -18,8 +18,10 @@ hipError_t interp(const float *x, const float *add, float *out, int C, int IH, i
 // writes [256][T] instead of [T][256]
 // slot = the device wall clock when the kernel runs (in-graph profiling)
 hipError_t stamp(unsigned long long *slot, hipStream_t s);
+// With row_mask set (no b), a row t with row_mask[t] == 0 is normalised as
+// if it were row_fill ([256]).
 hipError_t layernorm(const float *a, const float *b, const float *gamma, const float *beta, float *out, int T,
-                     int out_chw, hipStream_t s);
+                     int out_chw, hipStream_t s, const float *row_mask = nullptr, const float *row_fill = nullptr);
 // 8-head x 32 attention over token-major q/k/v (row strides in floats)
 hipError_t attention(const float *q, int ldq, const float *k, int ldk, const float *v, int ldv, float *out,
                      int ldo, int T, hipStream_t s);

@@ -62,6 +62,56 @@ __global__ __launch_bounds__(256) void k_dwconv(const float *__restrict__ x, con
     }
 }
 
+// The same depthwise conv without LDS, for the stride-2 downsampling convs on
+// large maps: a thread owns one output column of R consecutive output rows,
+// loads the (R - 1) * S + K input rows x K columns those outputs read (clamped
+// addresses, zero where the tap is padding) before the first FMA, and sums each
+// output's taps in (kh, kw) order as k_dwconv does, so the results are
+// bit-identical.  The LDS version stages a band with one load in flight per
+// thread at a time; here every load of a thread is issued together.
+template <int K, int S, int R>
+__global__ __launch_bounds__(256) void k_dwconv_rows(const float *__restrict__ x, const float *__restrict__ w,
+                                                     const float *__restrict__ b, float *__restrict__ out, int IH,
+                                                     int IW, int OH, int OW, int P, int act, int groups,
+                                                     int64_t in_plane, int64_t out_plane) {
+    constexpr int TR = (R - 1) * S + K;
+    const int c = blockIdx.y;
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= groups * OW) return;
+    const int g = i / OW, ox = i - g * OW;
+    const int oy0 = g * R, iy0 = oy0 * S - P, ix0 = ox * S - P;
+    const float *__restrict__ xc = x + (int64_t)c * in_plane;
+    float v[TR][K];
+#pragma unroll
+    for (int r = 0; r < TR; r++) {
+        const int iy = iy0 + r;
+        const bool ry = iy >= 0 && iy < IH;
+        const int64_t row = (int64_t)min(max(iy, 0), IH - 1) * IW;
+#pragma unroll
+        for (int kw = 0; kw < K; kw++) {
+            const int ix = ix0 + kw;
+            const float t = xc[row + min(max(ix, 0), IW - 1)];
+            v[r][kw] = (ry && ix >= 0 && ix < IW) ? t : 0.0f;
+        }
+    }
+    const float *__restrict__ wc = w + (int64_t)c * K * K;
+    float wk[K * K];
+#pragma unroll
+    for (int j = 0; j < K * K; j++) wk[j] = wc[j];
+    const float bc = b[c];
+    float *__restrict__ oc = out + (int64_t)c * out_plane + ox;
+#pragma unroll
+    for (int rr = 0; rr < R; rr++) {
+        const int oy = oy0 + rr;
+        float s = 0.0f;
+#pragma unroll
+        for (int kh = 0; kh < K; kh++)
+#pragma unroll
+            for (int kw = 0; kw < K; kw++) s = fmaf(v[rr * S + kh][kw], wk[kh * K + kw], s);
+        if (oy < OH) oc[(int64_t)oy * OW] = act_f(s + bc, act);
+    }
+}
+
 // 2x2 stride-1 max pool of x zero-padded by one column and one row at the
 // right/bottom (ggml_pad + ggml_pool_2d, src/ppdoclayout.cpp:621-626): the
 // output keeps x's size.
@@ -178,7 +228,8 @@ __global__ __launch_bounds__(256) void k_interp4(const float *__restrict__ x, co
 __global__ __launch_bounds__(256) void k_layernorm(const float *__restrict__ a, const float *__restrict__ b,
                                                    const float *__restrict__ gamma,
                                                    const float *__restrict__ beta, float *__restrict__ out,
-                                                   int T, float eps, int out_chw) {
+                                                   int T, float eps, int out_chw, const float *__restrict__ row_mask,
+                                                   const float *__restrict__ row_fill) {
     const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     if (t >= T) return;
@@ -188,8 +239,11 @@ __global__ __launch_bounds__(256) void k_layernorm(const float *__restrict__ a, 
     const float4 bv0 = *reinterpret_cast<const float4 *>((b ? b : a) + (int64_t)t * kDM + lane * 4);
     const float4 gv = *reinterpret_cast<const float4 *>(gamma + lane * 4);
     const float4 bv = *reinterpret_cast<const float4 *>(beta + lane * 4);
-    __builtin_amdgcn_sched_barrier(0);  // all four loads in flight before the reductions
-    float v[4] = {av.x, av.y, av.z, av.w};
+    // masked rows (row_mask[t] == 0) take row_fill instead of a's row
+    const float4 fv = *reinterpret_cast<const float4 *>((row_mask ? row_fill : a) + lane * 4);
+    const bool fill = row_mask && row_mask[t] == 0.0f;
+    __builtin_amdgcn_sched_barrier(0);  // all loads in flight before the reductions
+    float v[4] = {fill ? fv.x : av.x, fill ? fv.y : av.y, fill ? fv.z : av.z, fill ? fv.w : av.w};
     if (b) {
         v[0] += bv0.x;
         v[1] += bv0.y;
@@ -450,6 +504,20 @@ hipError_t dwconv(const float *x, const float *w, const float *b, float *out, in
     if (C < 1 || OH < 1 || OW < 1 || C > 65535 || max_rows < K || (K != 3 && K != 5) ||
         in_plane < (int64_t)IH * IW || out_plane < (int64_t)OH * OW)
         return hipErrorInvalidValue;
+    // stride 2 (the stage downsampling convs): the register version
+    // (PPDL_DW_ROWS=0 keeps the LDS one).  Graph A/B: -3 us per replay over
+    // the three downsampling convs.  With stride 1 (the 5x5 convs on the
+    // 50x50 and 25x25 maps, 2 rows per thread) it was 90 us slower: the LDS
+    // band there is read 25 times per element.
+    const char *er = getenv("PPDL_DW_ROWS");
+    if (K == 3 && S == 2 && !(er && er[0] == '0')) {
+        constexpr int R = 4;
+        const int groups = (OH + R - 1) / R;
+        const dim3 g2((unsigned)(((int64_t)groups * OW + 255) / 256), C);
+        hipLaunchKernelGGL((k_dwconv_rows<3, 2, R>), g2, dim3(256), 0, s, x, w, b, out, IH, IW, OH, OW, P, act,
+                           groups, in_plane, out_plane);
+        return hipGetLastError();
+    }
     const int bands = std::max(1, (2048 + C - 1) / C);
     const int RB = std::max(1, std::min((OH + bands - 1) / bands, (max_rows - K) / S + 1));
     const dim3 grid((OH + RB - 1) / RB, C);
@@ -495,11 +563,13 @@ hipError_t stamp(unsigned long long *slot, hipStream_t s) {
 }
 
 hipError_t layernorm(const float *a, const float *b, const float *gamma, const float *beta, float *out, int T,
-                     int out_chw, hipStream_t s) {
-    // rows, gamma, beta and (token-major) out are accessed as float4
-    if ((((uintptr_t)a | (uintptr_t)b | (uintptr_t)gamma | (uintptr_t)beta | (uintptr_t)out) & 15) != 0)
+                     int out_chw, hipStream_t s, const float *row_mask, const float *row_fill) {
+    // rows, gamma, beta, the fill row and (token-major) out are accessed as float4
+    if ((((uintptr_t)a | (uintptr_t)b | (uintptr_t)gamma | (uintptr_t)beta | (uintptr_t)out |
+          (uintptr_t)row_fill) & 15) != 0 || (row_mask && !row_fill) || (row_mask && b))
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_layernorm, dim3((T + 3) / 4), dim3(256), 0, s, a, b, gamma, beta, out, T, 1e-5f, out_chw);
+    hipLaunchKernelGGL(k_layernorm, dim3((T + 3) / 4), dim3(256), 0, s, a, b, gamma, beta, out, T, 1e-5f, out_chw,
+                       row_mask, row_fill);
     return hipGetLastError();
 }
 

@@ -277,3 +277,25 @@ def test_chained_winograd_transforms_match(gpu, model, image, monkeypatch):
             assert err <= TOL_OUTPUT, (k, err)
     finally:
         ctx.close()
+
+
+@pytest.mark.parametrize("knob", ["PPDL_DW_ROWS=0", "PPDL_MEMORY=1"])
+def test_exact_variants_match_default(gpu, model, image, monkeypatch, knob):
+    """Graph variants that must not change a bit: the depthwise conv with LDS
+    staging against the register version (the stride-2 convs), and the
+    source * valid multiply as its own node against the masked-row LayerNorm
+    that replaces it."""
+    import ppdoclayout as P
+
+    _, raw, _, _, _ = gpu
+    k, v = knob.split("=")
+    monkeypatch.setenv(k, v)
+    ctx = P.PPDocLayout(model[0], P.BACKEND_HIP)
+    try:
+        ctx.compute(image)
+        assert np.array_equal(ctx.raw(P.RAW_TOPK), raw["topk"])
+        for name, w in (("logits", P.RAW_LOGITS), ("boxes", P.RAW_BOXES), ("order", P.RAW_ORDER),
+                        ("masks", P.RAW_MASKS)):
+            assert np.array_equal(ctx.raw(w), raw[name]), (knob, name)
+    finally:
+        ctx.close()
