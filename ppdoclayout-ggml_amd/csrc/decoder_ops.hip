@@ -250,6 +250,8 @@ __global__ __launch_bounds__(256) void k_mask_box_bits(const uint32_t *__restric
 constexpr int kTopkThreads = 1024;
 constexpr int kTopkPer = 13;  // 13 * 1024 = 13312 >= 13125
 constexpr int kTopkSort = 512;
+constexpr int kTopkBins = 8192;  // histogram of the keys' top 13 bits (sign, exponent, 4 mantissa bits)
+constexpr int kTopkCap = 1024;   // most keys the one-histogram path ranks directly
 
 __device__ __forceinline__ uint64_t topk_key(float m, int idx) {
     m = m + 0.0f;  // -0 -> +0
@@ -281,6 +283,10 @@ __global__ __launch_bounds__(kTopkThreads) void k_topk(const float *__restrict__
     __shared__ uint32_t whist[kTopkThreads / 64][256];
     __shared__ uint64_t sel[kTopkSort];
     __shared__ int s_digit, s_rank, s_cnt, s_done;
+    __shared__ uint32_t fh[kTopkBins];
+    __shared__ uint64_t fsel[kTopkCap];
+    __shared__ uint32_t wsum[kTopkThreads / 64];
+    __shared__ int s_fbin, s_ftot;
     const int tid = threadIdx.x;
 
     uint64_t key[kTopkPer];
@@ -289,6 +295,71 @@ __global__ __launch_bounds__(kTopkThreads) void k_topk(const float *__restrict__
         const int t = tid + j * kTopkThreads;
         key[j] = 0;  // below every real key (real keys have a nonzero low word or high word)
         if (t < ntok) key[j] = keys ? keys[t] : topk_key(row_max(lg + (int64_t)t * nc, nc), t);
+    }
+
+    // One histogram over the keys' top 13 bits finds the bin that holds the
+    // nq-th largest key.  Every key of a higher bin is selected; when those
+    // and the threshold bin's keys number at most kTopkCap, they are gathered
+    // and each is placed by counting the gathered keys above it: every key
+    // above a gathered key is itself gathered, so that count is its rank.
+    // More keys than that (scores that crowd into one bin) take the radix
+    // select below.
+    {
+        const int lane = tid & 63, wv = tid >> 6;
+        for (int i = tid; i < kTopkBins; i += kTopkThreads) fh[i] = 0;
+        if (tid == 0) {
+            s_fbin = -1;
+            s_ftot = 0;
+            s_cnt = 0;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < kTopkPer; j++)
+            if (key[j] != 0) atomicAdd(&fh[(uint32_t)(key[j] >> 51)], 1u);
+        __syncthreads();
+        // counts from the top bin down: thread tid owns bins B-1-8tid .. B-8-8tid
+        constexpr int PB = kTopkBins / kTopkThreads;
+        uint32_t cb[PB], tot = 0;
+#pragma unroll
+        for (int b = 0; b < PB; b++) {
+            cb[b] = fh[kTopkBins - 1 - (tid * PB + b)];
+            tot += cb[b];
+        }
+        uint32_t incl = tot;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+            const uint32_t v = __shfl_up(incl, d);
+            if (lane >= d) incl += v;
+        }
+        if (lane == 63) wsum[wv] = incl;
+        __syncthreads();
+        uint32_t run = incl - tot;
+        for (int w = 0; w < wv; w++) run += wsum[w];
+#pragma unroll
+        for (int b = 0; b < PB; b++) {
+            if (run < (uint32_t)nq && run + cb[b] >= (uint32_t)nq) {
+                s_fbin = kTopkBins - 1 - (tid * PB + b);
+                s_ftot = (int)(run + cb[b]);
+            }
+            run += cb[b];
+        }
+        __syncthreads();
+        const int fbin = s_fbin, ftot = s_ftot;
+        if (fbin >= 0 && ftot <= kTopkCap) {
+#pragma unroll
+            for (int j = 0; j < kTopkPer; j++) {
+                if (key[j] != 0 && (int)(uint32_t)(key[j] >> 51) >= fbin) fsel[atomicAdd(&s_cnt, 1)] = key[j];
+            }
+            __syncthreads();
+            for (int i = tid; i < ftot; i += kTopkThreads) {
+                const uint64_t ki = fsel[i];
+                int r = 0;
+                for (int j = 0; j < ftot; j++) r += fsel[j] > ki ? 1 : 0;
+                if (r < nq) out[r] = (int32_t)(0xFFFFFFFFu - (uint32_t)(ki & 0xFFFFFFFFu));
+            }
+            return;
+        }
+        __syncthreads();  // s_cnt is reused below
     }
 
     // Radix select, most significant byte first.  Each pass histograms the

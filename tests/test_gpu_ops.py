@@ -833,6 +833,13 @@ def test_topk(hip, orc, with_ws):
     assert np.array_equal(run(tie, 300), orc.topk(tie, 300))
     small = rng.standard_normal((50, 3)).astype(np.float32)
     assert np.array_equal(run(small, 50), orc.topk(small, 50))
+    # scores crowded into one histogram bin (more keys than the direct ranking
+    # takes): the radix select
+    crowd = (100.0 + 1e-3 * rng.standard_normal((13125, 25))).astype(np.float32)
+    assert np.array_equal(run(crowd, 300), orc.topk(crowd, 300))
+    # a wide spread: the threshold bin holds few keys
+    wide = (rng.standard_normal((13125, 25)) * np.exp(4 * rng.standard_normal((13125, 1)))).astype(np.float32)
+    assert np.array_equal(run(wide, 300), orc.topk(wide, 300))
 
 
 # ---------------------------------------------------------------- tail balancing
