@@ -169,9 +169,33 @@ class Net {
 
    private:
     // ---- memory ----
+    // Buffers and weights are carved out of 256 MiB chunks (256-byte
+    // aligned, never freed before the context): a few large allocations
+    // instead of hundreds of small ones, so the graph's working set sits in
+    // few, large mappings.  Larger requests, and every request with
+    // PPDL_ARENA=0, get an allocation of their own.
+    static constexpr size_t kChunk = (size_t)256 << 20;
     float *alloc(int64_t nfloat) {
+        const size_t bytes = ((size_t)std::max<int64_t>(nfloat, 1) * 4 + 255) & ~(size_t)255;
+        const char *ea = getenv("PPDL_ARENA");
+        const bool arena = !(ea && ea[0] == '0');
         void *p = nullptr;
-        if (hipMalloc(&p, (size_t)std::max<int64_t>(nfloat, 1) * 4) != hipSuccess) {
+        if (arena && bytes <= kChunk) {
+            if (bytes > chunk_left_) {
+                if (hipMalloc(&p, kChunk) != hipSuccess) {
+                    oom_ = true;
+                    return nullptr;
+                }
+                allocs_.push_back(p);
+                chunk_ = (char *)p;
+                chunk_left_ = kChunk;
+            }
+            float *r = (float *)chunk_;
+            chunk_ += bytes;
+            chunk_left_ -= bytes;
+            return r;
+        }
+        if (hipMalloc(&p, bytes) != hipSuccess) {
             oom_ = true;
             return nullptr;
         }
@@ -335,6 +359,8 @@ class Net {
     Img csp(const Img &x, const std::string &pfx, float *out);
 
     std::vector<void *> allocs_;
+    char *chunk_ = nullptr;  // next free byte of the current chunk
+    size_t chunk_left_ = 0;
     std::map<std::string, float *> w_;
     std::map<std::string, std::vector<int64_t>> ne_;
     std::vector<Node> nodes_;
