@@ -301,7 +301,7 @@ __global__ __launch_bounds__(kThreads) void k_wg4_chain(const float *__restrict_
 // weights.
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-template <int OT, bool VW>
+template <int OT, bool VW, bool FULL>
 __global__ __launch_bounds__(384) void k_wg4_conv(const float *__restrict__ x, const float *__restrict__ wg4,
                                                  const float *__restrict__ bias, float *__restrict__ out, int IC,
                                                  int H, int W, int OC, int TW, int T, int act, int nocb, int vout) {
@@ -370,17 +370,21 @@ __global__ __launch_bounds__(384) void k_wg4_conv(const float *__restrict__ x, c
         float4 a[AL];
         uint32_t m;  // bits 0-5: patch rows inside; bit 6 + j: weight float4 j inside
     };
-    auto load = [&](Pre &pr, int st) {
-        st = min(st, last);
-        const int ic = 4 * st + q;
-        const float *__restrict__ xc = x + min(ic, IC - 1) * plane;
+    auto load = [&](Pre &pr, int su) {
+        // su past the last step: clamped addresses, all masks clear, so the
+        // step adds exact zeros
+        const int st = min(su, last);
+        const int ic = 4 * st + q, icu = 4 * su + q;
+        // 32-bit element offsets from the kernel-argument bases (uniform base
+        // + 32-bit lane offset: no 64-bit address per load kept live)
+        const uint32_t xo = (uint32_t)(min(ic, IC - 1) * plane);
 #pragma unroll
-        for (int r = 0; r < 6; r++) pr.d[r] = xc[prow[r]];
-        uint32_t m = ic < IC ? rowm : 0u;
+        for (int r = 0; r < 6; r++) pr.d[r] = x[xo + (uint32_t)prow[r]];
+        uint32_t m = icu < IC ? rowm : 0u;
 #pragma unroll
         for (int j = 0; j < AL; j++) {
-            const int icw = 4 * st + wk[j];
-            const float *src = wg4 + wbase[j] + min(icw, IC - 1) * OC;
+            const int icw = 4 * su + wk[j];
+            const float *src = wg4 + (uint32_t)(wbase[j] + min(4 * st + wk[j], IC - 1) * OC);
             if (VW) {
                 pr.a[j] = *reinterpret_cast<const float4 *>(src);
             } else {
@@ -389,7 +393,7 @@ __global__ __launch_bounds__(384) void k_wg4_conv(const float *__restrict__ x, c
                 pr.a[j].z = src[min(2, wlim[j])];
                 pr.a[j].w = src[min(3, wlim[j])];
             }
-            m |= (((wm >> j) & 1u) && icw < IC) ? (1u << (6 + j)) : 0u;
+            if (!FULL) m |= (((wm >> j) & 1u) && icw < IC) ? (1u << (6 + j)) : 0u;
         }
         pr.m = m;
     };
@@ -414,7 +418,9 @@ __global__ __launch_bounds__(384) void k_wg4_conv(const float *__restrict__ x, c
             const int quad = min(e, A4 - 1) % (OCB / 4);
             const int ocw = oc0 + 4 * quad;
             float4 v = pr.a[j];
-            const bool in = (pr.m >> (6 + j)) & 1u;
+            // FULL: every step inside IC, every quad inside OC (a float4 past
+            // the table lands in the pad), so no weight needs masking
+            const bool in = FULL || ((pr.m >> (6 + j)) & 1u);
             v.x = in ? v.x : 0.0f;
             v.y = (in && (VW || ocw + 1 < OC)) ? v.y : 0.0f;
             v.z = (in && (VW || ocw + 2 < OC)) ? v.z : 0.0f;
@@ -433,7 +439,9 @@ __global__ __launch_bounds__(384) void k_wg4_conv(const float *__restrict__ x, c
     // Prefetch ring: slot k holds the step congruent to k mod D.  Iteration s
     // runs the row stage of step s, stores step s + 1 (loaded D - 1
     // iterations earlier) into the other LDS buffer and reloads that slot
-    // with step s + 1 + D.  The loop is unrolled by D so slots are registers.
+    // with step s + 1 + D.  The loop is unrolled by D so slots are registers,
+    // and it runs whole groups of D steps (the steps past the last add
+    // zeros), so the loop has no exit between the unrolled steps.
     Pre pre[D];
 #pragma unroll
     for (int k = 0; k < D; k++) load(pre[k], k);
@@ -443,7 +451,6 @@ __global__ __launch_bounds__(384) void k_wg4_conv(const float *__restrict__ x, c
 #pragma unroll
         for (int k = 0; k < D; k++) {
             const int st = s0 + k;
-            if (st >= nsteps) break;  // uniform over the block
             const int buf = st & 1;
             __syncthreads();  // step st's column stage and weights are in LDS
             // row stage
@@ -567,16 +574,23 @@ hipError_t wg4_conv(const float *x, const float *wg4, const float *bias, float *
     // the kernel's input and weight offsets are 32-bit
     if ((int64_t)IC * H * W > 0x7fffffff || (int64_t)36 * IC * OC > 0x7fffffff) return hipErrorInvalidValue;
     const bool vw = OC % 4 == 0 && (((uintptr_t)wg4) & 15) == 0;
+    // no weight masks: whole 4-channel steps in whole groups of the kernel's
+    // 3-step prefetch ring, whole channel tiles per block
+    const int nsteps = (IC + 3) / 4;
+    const bool full = vw && IC % 4 == 0 && nsteps % 3 == 0 && OC % (16 * ot) == 0;
     const int vout = (W % 4 == 0 && (((uintptr_t)out) & 15) == 0) ? 1 : 0;
     const dim3 grid((unsigned)blocks), blk(384);
 #define PPDL_WG_LAUNCH(O)                                                                                        \
     do {                                                                                                         \
-        if (vw)                                                                                                  \
-            hipLaunchKernelGGL((k_wg4_conv<O, true>), grid, blk, 0, s, x, wg4, bias, out, IC, H, W, OC, TW, T, act, \
-                               nocb, vout);                                                                      \
-        else                                                                                                     \
-            hipLaunchKernelGGL((k_wg4_conv<O, false>), grid, blk, 0, s, x, wg4, bias, out, IC, H, W, OC, TW, T,  \
+        if (full)                                                                                                \
+            hipLaunchKernelGGL((k_wg4_conv<O, true, true>), grid, blk, 0, s, x, wg4, bias, out, IC, H, W, OC, TW, T, \
                                act, nocb, vout);                                                                 \
+        else if (vw)                                                                                             \
+            hipLaunchKernelGGL((k_wg4_conv<O, true, false>), grid, blk, 0, s, x, wg4, bias, out, IC, H, W, OC, TW, \
+                               T, act, nocb, vout);                                                              \
+        else                                                                                                     \
+            hipLaunchKernelGGL((k_wg4_conv<O, false, false>), grid, blk, 0, s, x, wg4, bias, out, IC, H, W, OC, TW, \
+                               T, act, nocb, vout);                                                              \
     } while (0)
     switch (ot) {
         case 1: PPDL_WG_LAUNCH(1); break;
