@@ -424,6 +424,155 @@ __global__ __launch_bounds__(kAttThreads) void k_attention(const float *__restri
     }
 }
 
+// The same attention with 16 queries per block on v_mfma_f32_16x16x4f32: twice
+// the blocks (152 for 300 tokens) and half the dependent MFMA chain per key
+// chunk.  Per 32-key chunk a wave computes two 16-key tiles of S^T = K Q^T
+// (lane l: query l%16, keys 4(l/16) + r of register r), and those registers
+// are the B operand of O^T += V^T P^T directly: step (tile t, register r)
+// contracts keys 16t + 4g + r, g = lane group, and the A operand reads V at
+// the same keys.  Loads, masking, the online softmax and the merge follow
+// k_attention.
+constexpr int kA16Q = 16;
+typedef float f32x4_att __attribute__((ext_vector_type(4)));
+
+__global__ __launch_bounds__(kAttThreads) void k_attention16(const float *__restrict__ q, int ldq,
+                                                             const float *__restrict__ k, int ldk,
+                                                             const float *__restrict__ v, int ldv,
+                                                             float *__restrict__ out, int ldo, int T, float scale) {
+    __shared__ float stage[2][kAttWaves][32][kHD + 1];  // K and V chunks per wave; then the merge tiles
+    __shared__ float mw[kAttWaves][kA16Q], lw[kAttWaves][kA16Q];
+    __shared__ float qs[kA16Q][kHD + 1];
+    float (*Ks)[32][kHD + 1] = stage[0];
+    float (*Vs)[32][kHD + 1] = stage[1];
+    float (*ow)[kHD][kA16Q + 1] = reinterpret_cast<float (*)[kHD][kA16Q + 1]>(&stage[0][0][0][0]);
+    const int h = blockIdx.y, q0 = blockIdx.x * kA16Q;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int c16 = lane & 15, g = lane >> 4;
+
+    const int row = lane >> 1, c0 = (lane & 1) * 16;
+    float4 kv[kAttCPW][8];
+#pragma unroll
+    for (int u = 0; u < kAttCPW; u++) {
+        const int s_ = min((wave + kAttWaves * u) * 32 + row, T - 1);
+        const float4 *kr = reinterpret_cast<const float4 *>(k + (int64_t)s_ * ldk + h * kHD + c0);
+        const float4 *vr = reinterpret_cast<const float4 *>(v + (int64_t)s_ * ldv + h * kHD + c0);
+#pragma unroll
+        for (int j = 0; j < 4; j++) kv[u][j] = kr[j], kv[u][4 + j] = vr[j];
+    }
+    if (threadIdx.x < kA16Q * kHD / 4) {
+        const int qi = threadIdx.x >> 3, d4 = (threadIdx.x & 7) * 4;
+        const float4 qv =
+            *reinterpret_cast<const float4 *>(q + (int64_t)min(q0 + qi, T - 1) * ldq + h * kHD + d4);
+        const bool in = q0 + qi < T;
+        qs[qi][d4 + 0] = in ? qv.x : 0.0f;
+        qs[qi][d4 + 1] = in ? qv.y : 0.0f;
+        qs[qi][d4 + 2] = in ? qv.z : 0.0f;
+        qs[qi][d4 + 3] = in ? qv.w : 0.0f;
+    }
+    __syncthreads();
+    // B operand of S^T: Q^T[d][q], lane supplies d = 4 st + g of query c16
+    float qf[kHD / 4];
+#pragma unroll
+    for (int st = 0; st < kHD / 4; st++) qf[st] = qs[c16][4 * st + g];
+    f32x4_att o[2];
+#pragma unroll
+    for (int t = 0; t < 2; t++) o[t] = f32x4_att{0.0f, 0.0f, 0.0f, 0.0f};
+    float m = -INFINITY, lsum = 0.0f;
+
+#pragma unroll
+    for (int u = 0; u < kAttCPW; u++) {
+        const int c = wave + kAttWaves * u;
+        if (c * 32 >= T) break;  // wave-uniform
+        const int key0 = c * 32;
+        {
+            const bool in = key0 + row < T;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const float4 a = kv[u][j], b = kv[u][4 + j];
+                Ks[wave][row][c0 + 4 * j + 0] = in ? a.x : 0.0f;
+                Ks[wave][row][c0 + 4 * j + 1] = in ? a.y : 0.0f;
+                Ks[wave][row][c0 + 4 * j + 2] = in ? a.z : 0.0f;
+                Ks[wave][row][c0 + 4 * j + 3] = in ? a.w : 0.0f;
+                Vs[wave][row][c0 + 4 * j + 0] = in ? b.x : 0.0f;
+                Vs[wave][row][c0 + 4 * j + 1] = in ? b.y : 0.0f;
+                Vs[wave][row][c0 + 4 * j + 2] = in ? b.z : 0.0f;
+                Vs[wave][row][c0 + 4 * j + 3] = in ? b.w : 0.0f;
+            }
+        }
+        __builtin_amdgcn_wave_barrier();
+        // S^T tiles: A = K (lane: key 16 t + c16, d = 4 st + g)
+        f32x4_att sc[2];
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            sc[t] = f32x4_att{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int st = 0; st < kHD / 4; st++)
+                sc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(Ks[wave][16 * t + c16][4 * st + g], qf[st], sc[t], 0, 0,
+                                                             0);
+        }
+        float mx = -INFINITY;
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int key = key0 + 16 * t + 4 * g + r;
+                sc[t][r] = key < T ? sc[t][r] * scale : -INFINITY;
+                mx = fmaxf(mx, sc[t][r]);
+            }
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float mn = fmaxf(m, mx);  // finite: the chunk holds at least one key < T
+        const float corr = expf(m - mn);
+        float ps = 0.0f;
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                sc[t][r] = expf(sc[t][r] - mn);
+                ps += sc[t][r];
+            }
+        ps += __shfl_xor(ps, 16);
+        ps += __shfl_xor(ps, 32);
+        lsum = lsum * corr + ps;
+        m = mn;
+#pragma unroll
+        for (int dt = 0; dt < 2; dt++) {
+#pragma unroll
+            for (int r = 0; r < 4; r++) o[dt][r] *= corr;
+#pragma unroll
+            for (int t = 0; t < 2; t++)
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+                    o[dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(Vs[wave][16 * t + 4 * g + r][16 * dt + c16], sc[t][r],
+                                                                 o[dt], 0, 0, 0);
+        }
+        __builtin_amdgcn_wave_barrier();
+    }
+
+    __syncthreads();  // every wave is done with its K/V slice (ow aliases it)
+    if (g == 0) {
+        mw[wave][c16] = m;
+        lw[wave][c16] = lsum;
+    }
+#pragma unroll
+    for (int dt = 0; dt < 2; dt++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) ow[wave][16 * dt + 4 * g + r][c16] = o[dt][r];
+    __syncthreads();
+    const int d = threadIdx.x & 31, qi = threadIdx.x >> 5, t = q0 + qi;  // 16 queries x 32 d = 512 threads
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kAttWaves; w++) M = fmaxf(M, mw[w][qi]);
+    float L = 0.0f, acc = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kAttWaves; w++) {
+        const float e = mw[w][qi] == -INFINITY ? 0.0f : expf(mw[w][qi] - M);
+        L += e * lw[w][qi];
+        acc += e * ow[w][d][qi];
+    }
+    if (t < T) out[(int64_t)t * ldo + h * kHD + d] = acc / L;
+}
+
 // ---------------------------------------------------------------------------
 // Elementwise helpers.
 __global__ __launch_bounds__(256) void k_add(const float *__restrict__ a, const float *__restrict__ b,
@@ -579,8 +728,14 @@ hipError_t attention(const float *q, int ldq, const float *k, int ldk, const flo
     if (T < 1 || T > kAttWaves * kAttCPW * 32 || ldk % 4 || ldv % 4 || ldq % 4 ||
         (((uintptr_t)k | (uintptr_t)v | (uintptr_t)q) & 15))
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_attention, dim3((T + kAttQ - 1) / kAttQ, kNH), dim3(kAttThreads), 0, s, q, ldq, k, ldk, v, ldv,
-                       out, ldo, T, 1.0f / sqrtf((float)kHD));
+    // 16 queries per block unless PPDL_ATT16=0
+    const char *e16 = getenv("PPDL_ATT16");
+    if (!(e16 && e16[0] == '0'))
+        hipLaunchKernelGGL(k_attention16, dim3((T + kA16Q - 1) / kA16Q, kNH), dim3(kAttThreads), 0, s, q, ldq, k, ldk,
+                           v, ldv, out, ldo, T, 1.0f / sqrtf((float)kHD));
+    else
+        hipLaunchKernelGGL(k_attention, dim3((T + kAttQ - 1) / kAttQ, kNH), dim3(kAttThreads), 0, s, q, ldq, k, ldk,
+                           v, ldv, out, ldo, T, 1.0f / sqrtf((float)kHD));
     return hipGetLastError();
 }
 

@@ -299,3 +299,32 @@ def test_exact_variants_match_default(gpu, model, image, monkeypatch, knob):
             assert np.array_equal(ctx.raw(w), raw[name]), (knob, name)
     finally:
         ctx.close()
+
+
+@pytest.mark.parametrize("knob", ["PPDL_ATT16=0"])
+def test_numeric_variants_match_default(gpu, model, image, monkeypatch, knob):
+    """Graph variants with another summation order: the attention with 32
+    queries per block (v_mfma_f32_32x32x2f32) against the default 16-query
+    kernel (v_mfma_f32_16x16x4f32).  Raw outputs within the network
+    tolerance, the same top-300 selection up to swaps of tied scores."""
+    import ppdoclayout as P
+
+    _, raw, _, _, _ = gpu
+    k, v = knob.split("=")
+    monkeypatch.setenv(k, v)
+    ctx = P.PPDocLayout(model[0], P.BACKEND_HIP)
+    try:
+        ctx.compute(image)
+        topk = ctx.raw(P.RAW_TOPK)
+        assert np.array_equal(np.sort(topk), np.sort(raw["topk"]))
+        pos = {int(t): i for i, t in enumerate(topk)}
+        p = np.array([pos[int(t)] for t in raw["topk"]])
+        for name, w in (("logits", P.RAW_LOGITS), ("boxes", P.RAW_BOXES), ("order", P.RAW_ORDER),
+                        ("masks", P.RAW_MASKS)):
+            got = ctx.raw(w)
+            got = got[p][:, p] if name == "order" else got[p]
+            err = normwise(got, raw[name])
+            say("%-10s %s vs default normwise %.3g" % (name, knob, err))
+            assert err <= TOL_OUTPUT, (knob, name, err)
+    finally:
+        ctx.close()
