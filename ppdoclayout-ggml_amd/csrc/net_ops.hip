@@ -219,6 +219,62 @@ __global__ __launch_bounds__(256) void k_interp4(const float *__restrict__ x, co
     *reinterpret_cast<float4 *>(out + o) = v;
 }
 
+// Exact 2x upsampling (OH = 2 IH, OW = 2 IW, OW % 4 == 0, 16-byte aligned out
+// and add), four outputs of one row per thread.  Nearest: input column ox / 2.
+// Bilinear: the scale is the constant 2, so the source coordinates are
+// (o + 0.5) / 2 - 0.5 exactly as in interp_at, and the four outputs
+// 4j .. 4j+3 read input columns 2j-1 .. 2j+2 (clamped) of two rows, loaded
+// once; each output is formed by interp_at's expression in its order, so the
+// values are bit-identical to k_interp4.  32-bit index math (the host checks
+// the extent).
+template <int BIL>
+__global__ __launch_bounds__(256) void k_up2x4(const float *__restrict__ x, const float *__restrict__ add,
+                                               float *__restrict__ out, int C, int IH, int IW) {
+    const int OH = 2 * IH, OW = 2 * IW, OW4 = OW / 4;
+    const uint32_t idx = blockIdx.x * 256u + threadIdx.x;
+    if (idx >= (uint32_t)C * (uint32_t)(OH * OW4)) return;
+    const uint32_t per = (uint32_t)(OH * OW4);
+    const uint32_t c = idx / per, rem = idx - c * per;
+    const int oy = (int)(rem / (uint32_t)OW4), j = (int)(rem - (uint32_t)oy * OW4), ox = 4 * j;
+    const float *__restrict__ xc = x + c * (uint32_t)(IH * IW);
+    float v[4];
+    if (!BIL) {
+        const float *r = xc + (oy >> 1) * IW + 2 * j;
+        const float a = r[0], b = r[1];
+        v[0] = a, v[1] = a, v[2] = b, v[3] = b;
+    } else {
+        const float fy = ((float)oy + 0.5f) / 2.0f - 0.5f;
+        const float fly = floorf(fy);
+        const int y0 = max(0, min((int)fly, IH - 1)), y1 = max(0, min((int)fly + 1, IH - 1));
+        const float dy = fmaxf(0.0f, fminf(fy - fly, 1.0f));
+        float r0[4], r1[4];  // columns 2j-1 .. 2j+2, clamped
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int cx = max(0, min(2 * j - 1 + e, IW - 1));
+            r0[e] = xc[y0 * IW + cx];
+            r1[e] = xc[y1 * IW + cx];
+        }
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const float fx = ((float)(ox + e) + 0.5f) / 2.0f - 0.5f;
+            const float flx = floorf(fx);
+            const float dx = fmaxf(0.0f, fminf(fx - flx, 1.0f));
+            const int l = (int)flx - (2 * j - 1);  // 0 or 1 or 2: the left column within r0 / r1
+            const float a = r0[l], bb = r0[l + 1], cc = r1[l], d = r1[l + 1];
+            v[e] = a * (1.0f - dx) * (1.0f - dy) + bb * dx * (1.0f - dy) + cc * (1.0f - dx) * dy + d * dx * dy;
+        }
+    }
+    const uint32_t o = (c * (uint32_t)OH + (uint32_t)oy) * (uint32_t)OW + (uint32_t)ox;
+    if (add) {
+        const float4 a = *reinterpret_cast<const float4 *>(add + o);
+        v[0] += a.x;
+        v[1] += a.y;
+        v[2] += a.z;
+        v[3] += a.w;
+    }
+    *reinterpret_cast<float4 *>(out + o) = make_float4(v[0], v[1], v[2], v[3]);
+}
+
 // ---------------------------------------------------------------------------
 // Layer norm over the 256 features of each token (ggml_norm eps 1e-5, then
 // * gamma + beta, src/ppdoclayout.cpp:550-554), with the residual sum of
@@ -690,6 +746,16 @@ hipError_t maxpool2_padend(const float *x, float *out, int C, int H, int W, hipS
 
 hipError_t interp(const float *x, const float *add, float *out, int C, int IH, int IW, int OH, int OW,
                   int bilinear, hipStream_t s) {
+    const char *eu = getenv("PPDL_UP2X");
+    if (!(eu && eu[0] == '0') && OH == 2 * IH && OW == 2 * IW && OW % 4 == 0 &&
+        (int64_t)C * OH * OW < (1LL << 31) && (((uintptr_t)out | (uintptr_t)add) & 15) == 0) {
+        const unsigned blocks = blocks_for((int64_t)C * OH * (OW / 4));
+        if (bilinear)
+            hipLaunchKernelGGL(k_up2x4<1>, dim3(blocks), dim3(256), 0, s, x, add, out, C, IH, IW);
+        else
+            hipLaunchKernelGGL(k_up2x4<0>, dim3(blocks), dim3(256), 0, s, x, add, out, C, IH, IW);
+        return hipGetLastError();
+    }
     if (OW % 4 == 0 && (((uintptr_t)out | (uintptr_t)add) & 15) == 0) {
         hipLaunchKernelGGL(k_interp4, dim3(blocks_for((int64_t)C * OH * (OW / 4))), dim3(256), 0, s, x, add, out, C,
                            IH, IW, OH, OW, bilinear);

@@ -279,12 +279,13 @@ def test_chained_winograd_transforms_match(gpu, model, image, monkeypatch):
         ctx.close()
 
 
-@pytest.mark.parametrize("knob", ["PPDL_DW_ROWS=0", "PPDL_MEMORY=1"])
+@pytest.mark.parametrize("knob", ["PPDL_DW_ROWS=0", "PPDL_MEMORY=1", "PPDL_UP2X=0"])
 def test_exact_variants_match_default(gpu, model, image, monkeypatch, knob):
     """Graph variants that must not change a bit: the depthwise conv with LDS
-    staging against the register version (the stride-2 convs), and the
+    staging against the register version (the stride-2 convs), the
     source * valid multiply as its own node against the masked-row LayerNorm
-    that replaces it."""
+    that replaces it, and the generic interpolation against the exact-2x
+    kernels (nearest and bilinear)."""
     import ppdoclayout as P
 
     _, raw, _, _, _ = gpu
