@@ -8,14 +8,30 @@
 
 namespace ppdl {
 
+// GELU (erf form) and sigmoid, kept out of line: the epilogues apply the
+// activation to many unrolled values, and the erf code inlined at each of
+// them multiplies the code a kernel fetches.
+__device__ __noinline__ float act_rare(float v, int act) {
+    if (act == kActGelu) return 0.5f * v * (1.0f + erff(v * 0.70710678118654752f));
+    return 1.0f / (1.0f + expf(-v));
+}
+
 // 0 none, 1 ReLU, 2 SiLU, 3 GELU (erf form), 4 sigmoid: ggml's relu / silu /
 // gelu_erf / sigmoid
 __device__ __forceinline__ float act_f(float v, int act) {
     if (act == kActRelu) return v > 0.0f ? v : 0.0f;
     if (act == kActSilu) return v / (1.0f + expf(-v));
-    if (act == kActGelu) return 0.5f * v * (1.0f + erff(v * 0.70710678118654752f));
-    if (act == kActSigmoid) return 1.0f / (1.0f + expf(-v));
+    if (act == kActGelu || act == kActSigmoid) return act_rare(v, act);
     return v;
+}
+
+// act_f with the activation fixed at compile time (A < 0: the runtime code
+// act): the same formulas, without the other activations' code in kernels
+// that apply it to many unrolled values.
+template <int A>
+__device__ __forceinline__ float act_t(float v, int act) {
+    if constexpr (A < 0) return act_f(v, act);
+    else return act_f(v, A);
 }
 
 // src/ppdoclayout.cpp:589-594: clamp to [0,1], log(max(x,1e-5)) - log(max(1-x,1e-5))
@@ -51,7 +67,9 @@ __device__ __forceinline__ float wave_sum(float x) {
 }
 
 // box refinement (src/ppdoclayout.cpp:860-862): sigmoid(delta + inv_sigmoid(ref))
-__device__ __forceinline__ float refine_box(float delta, float ref) {
+// Out of line for the same reason as act_rare: only the box-head GEMM's
+// epilogue takes it, and every epilogue would otherwise carry its code.
+__device__ __noinline__ float refine_box(float delta, float ref) {
     return 1.0f / (1.0f + expf(-(delta + inv_sigmoid(ref))));
 }
 

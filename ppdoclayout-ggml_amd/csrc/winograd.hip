@@ -135,7 +135,9 @@ __global__ __launch_bounds__(kThreads) void k_wg4_input(const float *__restrict_
     for (int p = 0; p < 36; p++) o[p * pstride] = v[p];
 }
 
-// add (optional, out's shape): a map added after the activation
+// add (optional, out's shape): a map added after the activation.  ACT: the
+// activation code fixed at compile time for the common ones (-1: runtime).
+template <int ACT>
 __global__ __launch_bounds__(kThreads) void k_wg4_output(const float *__restrict__ yt,
                                                          const float *__restrict__ bias,
                                                          const float *__restrict__ add,
@@ -160,7 +162,7 @@ __global__ __launch_bounds__(kThreads) void k_wg4_output(const float *__restrict
 #pragma unroll
     for (int i = 0; i < 4; i++)
 #pragma unroll
-        for (int j = 0; j < 4; j++) Y[i][j] = act_f(Y[i][j] + b, act);
+        for (int j = 0; j < 4; j++) Y[i][j] = act_t<ACT>(Y[i][j] + b, act);
 
     float *__restrict__ oplane = out + (int64_t)oc * OH * OW;
     const float *__restrict__ aplane = add ? add + (int64_t)oc * OH * OW : nullptr;
@@ -643,8 +645,20 @@ hipError_t wg4_output(const float *yt, const float *bias, const float *add, floa
                       int OW, int OH, int act, int ldt, hipStream_t s) {
     const int64_t n = (int64_t)TW * TH * OC;
     const unsigned blocks = (unsigned)((n + kThreads - 1) / kThreads);
-    hipLaunchKernelGGL(k_wg4_output, dim3(blocks), dim3(kThreads), 0, s, yt, bias, add, out, TW, TH, OC,
-                       OW, OH, act, ldt);
+    switch (act) {
+        case kActNone:
+            hipLaunchKernelGGL(k_wg4_output<kActNone>, dim3(blocks), dim3(kThreads), 0, s, yt, bias, add, out, TW, TH,
+                               OC, OW, OH, act, ldt);
+            break;
+        case kActSilu:
+            hipLaunchKernelGGL(k_wg4_output<kActSilu>, dim3(blocks), dim3(kThreads), 0, s, yt, bias, add, out, TW, TH,
+                               OC, OW, OH, act, ldt);
+            break;
+        default:
+            hipLaunchKernelGGL(k_wg4_output<-1>, dim3(blocks), dim3(kThreads), 0, s, yt, bias, add, out, TW, TH, OC,
+                               OW, OH, act, ldt);
+            break;
+    }
     return hipGetLastError();
 }
 
