@@ -569,10 +569,17 @@ bool Net::concat_linears(GgufFile &g, const std::vector<std::string> &parts, con
 // vs 24.8 us), 64 -> 64 @200 (52.9 vs 39.1) and every 256-channel conv (61 vs
 // 20-63 us in isolation) are faster as three ops.  PPDL_WG_FUSED=0 / 1 forces
 // either path for every k3 s1 p1 conv (read at graph build).
+// With the kernel's unmasked-weight form and whole prefetch groups, 96- and
+// 128-channel inputs to 96 outputs at 100x100 (stage 1's six convs) also
+// favour it in isolation: 96 -> 96 25.4 against 30.7 us, 128 -> 96 33.3
+// against 35.8 us (64 -> 64 @100 21.2 / 21.8); 64 -> 64 and 128 -> 64 @200
+// stay three ops.  PPDL_WG_FUSED_WIDE=0 keeps only the 48-channel rule.
 bool wg_fused(int IC, int H, int W, int OC) {
     if (const char *e = getenv("PPDL_WG_FUSED")) return e[0] == '1';
     const int64_t T = (int64_t)((W + 3) / 4) * ((H + 3) / 4);
-    return IC <= 96 && OC <= 48 && T >= 625;
+    const char *ew = getenv("PPDL_WG_FUSED_WIDE");
+    const bool wide = !(ew && ew[0] == '0') && IC <= 128 && OC <= 96 && T >= 625 && T <= 1024;
+    return (IC <= 96 && OC <= 48 && T >= 625) || wide;
 }
 
 // ---------------------------------------------------------------------------
