@@ -1140,9 +1140,20 @@ __global__ __launch_bounds__(128) void k_conv_k3s2(GemmArgs g) {
     __shared__ float bs[32];
     const int M = g.M, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t lda = (uint32_t)g.lda;
-    for (int i = tid; i < 32 * KP; i += 128) {
-        const int k = i >> 5, m = i & 31;
-        ws[m * KP + k] = (m < M && k < KK) ? g.A[(uint32_t)k * lda + (uint32_t)m] : 0.0f;
+    // all of a thread's weight loads issued together: clamped addresses, the
+    // padding zeroed by select (a load under a condition is waited for before
+    // the next iteration's)
+    constexpr int WI = (32 * KP + 127) / 128;
+    float wv[WI];
+#pragma unroll
+    for (int u = 0; u < WI; u++) {
+        const int i = min(tid + 128 * u, 32 * KP - 1), k = i >> 5, m = i & 31;
+        wv[u] = g.A[(uint32_t)min(k, KK - 1) * lda + (uint32_t)min(m, M - 1)];
+    }
+#pragma unroll
+    for (int u = 0; u < WI; u++) {
+        const int i = tid + 128 * u, k = i >> 5, m = i & 31;
+        if (i < 32 * KP) ws[m * KP + k] = (m < M && k < KK) ? wv[u] : 0.0f;
     }
     if (tid < 32) bs[tid] = (g.bias && tid < M) ? g.bias[tid] : 0.0f;
     __syncthreads();
