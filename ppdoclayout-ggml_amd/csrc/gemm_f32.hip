@@ -1086,6 +1086,125 @@ __global__ __launch_bounds__(64 * WV) void k_conv_frag(GemmArgs g) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// k2 s1 p0 convs with 16 or 32 input and at most 32 output channels, OW and
+// IW multiples of 4 (the stem's 2x2 convs at 400x400, bottom / right padding
+// by clamping), on v_mfma_f32_16x16x4f32.  A lane owns a quad of 4
+// consecutive output pixels of one row (lane l: quad l % 16 of the wave's 16)
+// and channel slot l / 16 (4 input channels per MFMA step).  Per input row
+// (kh) and channel quad, one float4 of the row plus the next column give the
+// 5 input values both column taps of the 4 pixels read, so two input loads
+// and two weight loads per 16-channel tile feed 8 MFMAs (4 accumulators per
+// tile, one per pixel of the quad); all of a row's loads are issued before
+// its MFMAs.  Register r of an accumulator holds output channel
+// 16 t + 4 (l / 16) + r of quad l % 16, so the 4 accumulators give a float4
+// of 4 consecutive pixels per register.  The fragment kernel (32-row tiles,
+// one value per operand per MFMA, half-empty tiles at 16 output channels)
+// took 30.7 / 21.7 us at 32 -> 16 / 16 -> 32 @400x400.
+typedef float f32x4_k2q __attribute__((ext_vector_type(4)));
+
+template <int IC, int MT>
+__global__ __launch_bounds__(256) void k_conv_k2q(GemmArgs g) {
+    constexpr int NQC = IC / 4;  // channel quads
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int c16 = lane & 15, g4 = lane >> 4;
+    const int OW = g.OW, IW = g.IW, IH = g.IH, M = g.M;
+    const int QW = OW >> 2, NQ = g.N >> 2;
+    const int qd = (xcd_remap(blockIdx.x, gridDim.x) * 4 + wave) * 16 + c16;
+    const int qc = min(qd, NQ - 1);
+    const int oy = qc / QW, ox0 = 4 * (qc - oy * QW);
+    const uint32_t plane = (uint32_t)IH * (uint32_t)IW, lda = (uint32_t)g.lda;
+    uint32_t mc[MT];
+    bool m_ok[MT];
+#pragma unroll
+    for (int t = 0; t < MT; t++) mc[t] = (uint32_t)min(16 * t + c16, M - 1), m_ok[t] = 16 * t + c16 < M;
+    const bool e_in = ox0 + 4 < IW;
+    const uint32_t ecol = (uint32_t)min(ox0 + 4, IW - 1) - (uint32_t)ox0;
+    const float *__restrict__ X = g.B;
+    const float *__restrict__ Wt = g.A;
+    f32x4_k2q acc[MT][4];
+#pragma unroll
+    for (int t = 0; t < MT; t++)
+#pragma unroll
+        for (int q = 0; q < 4; q++) acc[t][q] = f32x4_k2q{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int kh = 0; kh < 2; kh++) {
+        const int iy = oy + kh;
+        const bool rin = iy < IH;
+        const uint32_t rowo = (uint32_t)min(iy, IH - 1) * (uint32_t)IW + (uint32_t)ox0;
+        float4 v[NQC];
+        float e[NQC], a0[MT][NQC], a1[MT][NQC];
+#pragma unroll
+        for (int p = 0; p < NQC; p++) {
+            const uint32_t ic = (uint32_t)(4 * p + g4);
+            const float *xr = X + ic * plane + rowo;
+            v[p] = *reinterpret_cast<const float4 *>(xr);
+            e[p] = xr[ecol];
+#pragma unroll
+            for (int t = 0; t < MT; t++) {
+                a0[t][p] = Wt[((uint32_t)(2 * kh) * (uint32_t)IC + ic) * lda + mc[t]];
+                a1[t][p] = Wt[((uint32_t)(2 * kh + 1) * (uint32_t)IC + ic) * lda + mc[t]];
+            }
+        }
+#pragma unroll
+        for (int p = 0; p < NQC; p++) {
+            const float x[5] = {rin ? v[p].x : 0.0f, rin ? v[p].y : 0.0f, rin ? v[p].z : 0.0f, rin ? v[p].w : 0.0f,
+                                (rin && e_in) ? e[p] : 0.0f};
+#pragma unroll
+            for (int t = 0; t < MT; t++) {
+                const float w0 = m_ok[t] ? a0[t][p] : 0.0f, w1 = m_ok[t] ? a1[t][p] : 0.0f;
+#pragma unroll
+                for (int q = 0; q < 4; q++)
+                    acc[t][q] = __builtin_amdgcn_mfma_f32_16x16x4f32(w0, x[q], acc[t][q], 0, 0, 0);
+#pragma unroll
+                for (int q = 0; q < 4; q++)
+                    acc[t][q] = __builtin_amdgcn_mfma_f32_16x16x4f32(w1, x[q + 1], acc[t][q], 0, 0, 0);
+            }
+        }
+    }
+    if (qd >= NQ) return;
+    float *__restrict__ C = g.C;
+    const uint32_t ldc = (uint32_t)g.ldc, px = (uint32_t)oy * (uint32_t)OW + (uint32_t)ox0;
+#pragma unroll
+    for (int t = 0; t < MT; t++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int m = 16 * t + 4 * g4 + r;
+            if (m < M) {
+                const float b = g.bias ? g.bias[m] : 0.0f;
+                const float4 o = make_float4(act_f(acc[t][0][r] + b, g.act), act_f(acc[t][1][r] + b, g.act),
+                                             act_f(acc[t][2][r] + b, g.act), act_f(acc[t][3][r] + b, g.act));
+                *reinterpret_cast<float4 *>(C + (uint32_t)m * ldc + px) = o;
+            }
+        }
+}
+
+// The quad kernel's cases (PPDL_CONV_K2Q=0 turns it off).
+bool k2q_ok(const GemmArgs &g) {
+    const char *e = getenv("PPDL_CONV_K2Q");
+    if (e && e[0] == '0') return false;
+    const auto a16 = [](const void *q) { return (((uintptr_t)q) & 15) == 0; };
+    return g.KW == 2 && g.S == 1 && g.P == 0 && (g.IC == 16 || g.IC == 32) && g.M >= 1 && g.M <= 32 &&
+           !g.a_rowmajor && !g.c_trans && g.add_mode == 0 && !g.add && g.batch == 1 && g.OW >= 4 && g.OW % 4 == 0 &&
+           g.IW % 4 == 0 && g.OW <= g.IW && g.N % g.OW == 0 && g.N / g.OW <= g.IH && g.ldc % 4 == 0 && g.ldc >= g.N &&
+           a16(g.B) && a16(g.C) && (int64_t)g.IC * g.IH * g.IW < (1LL << 31) &&
+           (int64_t)4 * g.IC * g.lda < (1LL << 31) && (int64_t)32 * g.ldc < (1LL << 31);
+}
+
+hipError_t launch_k2q(const GemmArgs &g, hipStream_t s) {
+    const int64_t quads = g.N / 4, blocks = (quads + 63) / 64;  // 16 quads per wave
+    if (blocks > 0x7fffffff) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)blocks);
+    if (g.M <= 16) {
+        if (g.IC == 16) hipLaunchKernelGGL((k_conv_k2q<16, 1>), grid, dim3(256), 0, s, g);
+        else hipLaunchKernelGGL((k_conv_k2q<32, 1>), grid, dim3(256), 0, s, g);
+    } else {
+        if (g.IC == 16) hipLaunchKernelGGL((k_conv_k2q<16, 2>), grid, dim3(256), 0, s, g);
+        else hipLaunchKernelGGL((k_conv_k2q<32, 2>), grid, dim3(256), 0, s, g);
+    }
+    return hipGetLastError();
+}
+
 // The fragment kernel serves op 16 with at most 32 output channels (the stem
 // convs), plain bias + act into a CHW output.  PPDL_CONV_FRAG=0 turns it off.
 bool frag_ok(const GemmArgs &g) {
@@ -2004,6 +2123,7 @@ hipError_t dispatch(const GemmArgs &g_in, const GemmWorkspace &ws, hipStream_t s
     if (BMODE == 1) {
         if (const int cc = patch_cc(g)) return launch_patch(g, cc, s);
         if (direct_ok(g)) return launch_direct(g, s);
+        if (k2q_ok(g)) return launch_k2q(g, s);
         if (frag_ok(g)) return launch_frag(g, s);
     }
     if (g.a_w4) {
@@ -2084,7 +2204,7 @@ GemmPlan gemm_plan(const GemmArgs &g, int64_t ws_bytes, bool im2col) {
 
 int64_t gemm_ws_bytes_for(const GemmArgs &g, bool im2col) {
     if (g.a_w4 || g.ln_g) return 0;  // the small kernel, no split-K
-    if (im2col && !patch_cc(g) && (direct_ok(g) || frag_ok(g))) return 0;  // neither kernel uses a workspace
+    if (im2col && !patch_cc(g) && (direct_ok(g) || k2q_ok(g) || frag_ok(g))) return 0;  // no workspace
     const GemmPlan p = gemm_plan(g, INT64_MAX, im2col);
     return gemm_ws_bytes(g.M, g.N, g.batch, p.cfg, p.splits);
 }
@@ -2094,6 +2214,7 @@ hipError_t gemm_dense(const GemmArgs &g, const GemmWorkspace &ws, hipStream_t s)
 std::string gemm_kernel_name(const GemmArgs &g, int64_t ws_bytes, bool im2col) {
     if (im2col && patch_cc(g)) return g.KW == 3 ? "k_conv_patch<3, 2>" : "k_conv_patch<2, 1>";
     if (im2col && direct_ok(g)) return "k_conv_k3s2<" + std::to_string(g.IC) + ">";
+    if (im2col && k2q_ok(g)) return "k_conv_k2q<" + std::to_string(g.IC) + (g.M <= 16 ? ", 1>" : ", 2>");
     if (im2col && frag_ok(g)) return "k_conv_frag<" + std::to_string(frag_waves(g)) + ">";
     if (g.a_w4 && small16_ok(g, 2)) return "k_gemm_small16<2, 8, false, false>";
     if (g.a_w4) return "k_gemm_small<2, " + std::to_string(small_waves(g.K, small_tiles(g))) + ", false>";

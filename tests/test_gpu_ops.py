@@ -542,6 +542,38 @@ def test_conv_patch_kernel(hip, orc, IC, H, W, OC, K, S, P, PE, monkeypatch):
     assert normwise(outs[0], outs[1]) < TOL
 
 
+@pytest.mark.parametrize("IC,H,W,OC,PE", [
+    (32, 400, 400, 16, 1),   # stem2a
+    (16, 400, 400, 32, 1),   # stem2b
+    (16, 12, 16, 20, 1),     # ragged output channels, 4 quads per row
+    (32, 5, 4, 32, 1),       # one quad per row, bottom padding row
+    (16, 9, 20, 7, 1),       # quads of a wave span several rows
+])
+@pytest.mark.parametrize("act", [0, 1])
+def test_conv_k2q_kernel(hip, orc, IC, H, W, OC, PE, act, monkeypatch):
+    """Op 16 k2 s1 with 16 or 32 input channels, <= 32 output channels and
+    widths a multiple of 4 (the stem's 2x2 convs) on the quad kernel: against float64 with the bottom /
+    right zero padding, and against the fragment kernel (PPDL_CONV_K2Q=0)."""
+    say(f"k2q conv {IC}->{OC} @{H}x{W} pe{PE} act{act}")
+    rng = np.random.default_rng(IC * 13 + OC + H + W + act)
+    x, w, b = conv_inputs(rng, IC, H, W, OC, 2)
+    wr, _ = hip.repack_conv(w)
+    OH, OW = H + PE - 1, W + PE - 1
+    p14 = 2 | (1 << 8) | (0 << 16) | (act << 24)
+    outs = []
+    for flag, kern in (("1", "k_conv_k2q"), ("0", "k_conv_frag<")):
+        monkeypatch.setenv("PPDL_CONV_K2Q", flag)
+        out = torch.full((OC, OH, OW), float("nan"), device="cuda")
+        srcs = [dev(x), dev(wr), dev(b)]
+        assert hip.kernel_name(hip.OP_CONV_IM2COL, out, srcs, p14, PE).startswith(kern)
+        hip.run_checked(hip.OP_CONV_IM2COL, out, srcs, p14, PE)
+        outs.append(host(out))
+    xp = np.pad(x, ((0, 0), (0, PE), (0, PE)))
+    ref = orc.conv2d_f64(xp, w, b, 1, 0, act)
+    assert np.isfinite(outs[0]).all()
+    assert normwise(outs[0], ref) < TOL and normwise(outs[1], ref) < TOL
+
+
 # ---------------------------------------------------------------- fused F(4,3) conv (op 17)
 def hip_wg4_conv(hip, x, w, b, act):
     _, wg4 = hip.repack_conv(w)
