@@ -1179,6 +1179,126 @@ __global__ __launch_bounds__(256) void k_conv_k2q(GemmArgs g) {
         }
 }
 
+// k3 s2 p1 convs with 64 input and at most 32 output channels (the stem's
+// 64 -> 32 conv at 400 -> 200), the same quad scheme: the 4 output pixels of
+// a lane read input columns 2 ox0 - 1 .. 2 ox0 + 7 of each of the 3 rows, one
+// scalar and two float4 loads, which feed all 3 column taps (tap kw of pixel
+// q is element 2 q + kw).  K = 576 is long for one wave, so the block's 4
+// waves take a quarter of the input channels each for the same 16 quads and
+// add their tiles through LDS in wave order.
+template <int IC, int MT>
+__global__ __launch_bounds__(256) void k_conv_k3s2q(GemmArgs g) {
+    constexpr int NQC = IC / 16;  // channel quads per wave
+    __shared__ float red[3][MT * 16][64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int c16 = lane & 15, g4 = lane >> 4;
+    const int OW = g.OW, IW = g.IW, IH = g.IH, M = g.M;
+    const int QW = OW >> 2, NQ = g.N >> 2;
+    const int qd = xcd_remap(blockIdx.x, gridDim.x) * 16 + c16;
+    const int qc = min(qd, NQ - 1);
+    const int oy = qc / QW, ox0 = 4 * (qc - oy * QW);
+    const uint32_t plane = (uint32_t)IH * (uint32_t)IW, lda = (uint32_t)g.lda;
+    uint32_t mc[MT];
+    bool m_ok[MT];
+#pragma unroll
+    for (int t = 0; t < MT; t++) mc[t] = (uint32_t)min(16 * t + c16, M - 1), m_ok[t] = 16 * t + c16 < M;
+    const bool l_in = ox0 > 0;  // column 2 ox0 - 1 inside the image
+    const uint32_t c1 = (uint32_t)(2 * ox0);  // first float4 column
+    const float *__restrict__ X = g.B;
+    const float *__restrict__ Wt = g.A;
+    f32x4_k2q acc[MT][4];
+#pragma unroll
+    for (int t = 0; t < MT; t++)
+#pragma unroll
+        for (int q = 0; q < 4; q++) acc[t][q] = f32x4_k2q{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int kh = 0; kh < 3; kh++) {
+        const int iy = 2 * oy - 1 + kh;
+        const bool rin = iy >= 0 && iy < IH;
+        const uint32_t rowo = (uint32_t)min(max(iy, 0), IH - 1) * (uint32_t)IW;
+        float4 v0[NQC], v1[NQC];
+        float xl[NQC], a[MT][3][NQC];
+#pragma unroll
+        for (int p = 0; p < NQC; p++) {
+            const uint32_t ic = (uint32_t)(4 * (wave * NQC + p) + g4);
+            const float *xr = X + ic * plane + rowo;
+            xl[p] = xr[l_in ? c1 - 1 : c1];
+            v0[p] = *reinterpret_cast<const float4 *>(xr + c1);
+            v1[p] = *reinterpret_cast<const float4 *>(xr + c1 + 4);
+#pragma unroll
+            for (int kw = 0; kw < 3; kw++)
+#pragma unroll
+                for (int t = 0; t < MT; t++) a[t][kw][p] = Wt[((uint32_t)(kh * 3 + kw) * (uint32_t)IC + ic) * lda + mc[t]];
+        }
+#pragma unroll
+        for (int p = 0; p < NQC; p++) {
+            const float x[9] = {(rin && l_in) ? xl[p] : 0.0f, rin ? v0[p].x : 0.0f, rin ? v0[p].y : 0.0f,
+                                rin ? v0[p].z : 0.0f,         rin ? v0[p].w : 0.0f, rin ? v1[p].x : 0.0f,
+                                rin ? v1[p].y : 0.0f,         rin ? v1[p].z : 0.0f, rin ? v1[p].w : 0.0f};
+#pragma unroll
+            for (int kw = 0; kw < 3; kw++)
+#pragma unroll
+                for (int t = 0; t < MT; t++) {
+                    const float w = m_ok[t] ? a[t][kw][p] : 0.0f;
+#pragma unroll
+                    for (int q = 0; q < 4; q++)
+                        acc[t][q] = __builtin_amdgcn_mfma_f32_16x16x4f32(w, x[2 * q + kw], acc[t][q], 0, 0, 0);
+                }
+        }
+    }
+    // waves 1-3 hand their tiles to wave 0 (register t * 16 + q * 4 + r)
+    if (wave > 0)
+#pragma unroll
+        for (int t = 0; t < MT; t++)
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) red[wave - 1][t * 16 + q * 4 + r][lane] = acc[t][q][r];
+    __syncthreads();
+    if (wave > 0 || qd >= NQ) return;
+#pragma unroll
+    for (int w = 0; w < 3; w++)
+#pragma unroll
+        for (int t = 0; t < MT; t++)
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) acc[t][q][r] += red[w][t * 16 + q * 4 + r][lane];
+    float *__restrict__ C = g.C;
+    const uint32_t ldc = (uint32_t)g.ldc, px = (uint32_t)oy * (uint32_t)OW + (uint32_t)ox0;
+#pragma unroll
+    for (int t = 0; t < MT; t++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int m = 16 * t + 4 * g4 + r;
+            if (m < M) {
+                const float b = g.bias ? g.bias[m] : 0.0f;
+                const float4 o = make_float4(act_f(acc[t][0][r] + b, g.act), act_f(acc[t][1][r] + b, g.act),
+                                             act_f(acc[t][2][r] + b, g.act), act_f(acc[t][3][r] + b, g.act));
+                *reinterpret_cast<float4 *>(C + (uint32_t)m * ldc + px) = o;
+            }
+        }
+}
+
+bool k3s2q_ok(const GemmArgs &g) {
+    const char *e = getenv("PPDL_CONV_K2Q");
+    if (e && e[0] == '0') return false;
+    const auto a16 = [](const void *q) { return (((uintptr_t)q) & 15) == 0; };
+    return g.KW == 3 && g.S == 2 && g.P == 1 && g.IC == 64 && g.M >= 1 && g.M <= 32 && !g.a_rowmajor &&
+           !g.c_trans && g.add_mode == 0 && !g.add && g.batch == 1 && g.OW >= 4 && g.OW % 4 == 0 &&
+           g.IW % 4 == 0 && 2 * g.OW <= g.IW && g.N % g.OW == 0 && g.ldc % 4 == 0 && g.ldc >= g.N && a16(g.B) &&
+           a16(g.C) && (int64_t)g.IC * g.IH * g.IW < (1LL << 31) && (int64_t)9 * g.IC * g.lda < (1LL << 31) &&
+           (int64_t)32 * g.ldc < (1LL << 31);
+}
+
+hipError_t launch_k3s2q(const GemmArgs &g, hipStream_t s) {
+    const int64_t blocks = (g.N / 4 + 15) / 16;  // 16 quads per block
+    if (blocks > 0x7fffffff) return hipErrorInvalidValue;
+    if (g.M <= 16) hipLaunchKernelGGL((k_conv_k3s2q<64, 1>), dim3((unsigned)blocks), dim3(256), 0, s, g);
+    else hipLaunchKernelGGL((k_conv_k3s2q<64, 2>), dim3((unsigned)blocks), dim3(256), 0, s, g);
+    return hipGetLastError();
+}
+
 // The quad kernel's cases (PPDL_CONV_K2Q=0 turns it off).
 bool k2q_ok(const GemmArgs &g) {
     const char *e = getenv("PPDL_CONV_K2Q");
@@ -2124,6 +2244,7 @@ hipError_t dispatch(const GemmArgs &g_in, const GemmWorkspace &ws, hipStream_t s
         if (const int cc = patch_cc(g)) return launch_patch(g, cc, s);
         if (direct_ok(g)) return launch_direct(g, s);
         if (k2q_ok(g)) return launch_k2q(g, s);
+        if (k3s2q_ok(g)) return launch_k3s2q(g, s);
         if (frag_ok(g)) return launch_frag(g, s);
     }
     if (g.a_w4) {
@@ -2204,7 +2325,7 @@ GemmPlan gemm_plan(const GemmArgs &g, int64_t ws_bytes, bool im2col) {
 
 int64_t gemm_ws_bytes_for(const GemmArgs &g, bool im2col) {
     if (g.a_w4 || g.ln_g) return 0;  // the small kernel, no split-K
-    if (im2col && !patch_cc(g) && (direct_ok(g) || k2q_ok(g) || frag_ok(g))) return 0;  // no workspace
+    if (im2col && !patch_cc(g) && (direct_ok(g) || k2q_ok(g) || k3s2q_ok(g) || frag_ok(g))) return 0;  // no workspace
     const GemmPlan p = gemm_plan(g, INT64_MAX, im2col);
     return gemm_ws_bytes(g.M, g.N, g.batch, p.cfg, p.splits);
 }
@@ -2215,6 +2336,7 @@ std::string gemm_kernel_name(const GemmArgs &g, int64_t ws_bytes, bool im2col) {
     if (im2col && patch_cc(g)) return g.KW == 3 ? "k_conv_patch<3, 2>" : "k_conv_patch<2, 1>";
     if (im2col && direct_ok(g)) return "k_conv_k3s2<" + std::to_string(g.IC) + ">";
     if (im2col && k2q_ok(g)) return "k_conv_k2q<" + std::to_string(g.IC) + (g.M <= 16 ? ", 1>" : ", 2>");
+    if (im2col && k3s2q_ok(g)) return std::string("k_conv_k3s2q<64, ") + (g.M <= 16 ? "1>" : "2>");
     if (im2col && frag_ok(g)) return "k_conv_frag<" + std::to_string(frag_waves(g)) + ">";
     if (g.a_w4 && small16_ok(g, 2)) return "k_gemm_small16<2, 8, false, false>";
     if (g.a_w4) return "k_gemm_small<2, " + std::to_string(small_waves(g.K, small_tiles(g))) + ", false>";

@@ -574,6 +574,32 @@ def test_conv_k2q_kernel(hip, orc, IC, H, W, OC, PE, act, monkeypatch):
     assert normwise(outs[0], ref) < TOL and normwise(outs[1], ref) < TOL
 
 
+@pytest.mark.parametrize("H,W,OC", [(400, 400, 32), (12, 16, 20), (9, 8, 32), (10, 24, 7)])
+@pytest.mark.parametrize("act", [0, 1])
+def test_conv_k3s2q_kernel(hip, orc, H, W, OC, act, monkeypatch):
+    """Op 16 k3 s2 p1 with 64 input and <= 32 output channels (the stem's
+    64 -> 32 conv) on the quad kernel with its four-way channel split: against
+    float64, and against the fragment kernel (PPDL_CONV_K2Q=0)."""
+    IC = 64
+    say(f"k3s2q conv {IC}->{OC} @{H}x{W} act{act}")
+    rng = np.random.default_rng(OC + H + W + act)
+    x, w, b = conv_inputs(rng, IC, H, W, OC, 3)
+    wr, _ = hip.repack_conv(w)
+    OH, OW = (H + 2 - 3) // 2 + 1, (W + 2 - 3) // 2 + 1
+    p14 = 3 | (2 << 8) | (1 << 16) | (act << 24)
+    outs = []
+    for flag, kern in (("1", "k_conv_k3s2q"), ("0", "k_conv_frag<")):
+        monkeypatch.setenv("PPDL_CONV_K2Q", flag)
+        out = torch.full((OC, OH, OW), float("nan"), device="cuda")
+        srcs = [dev(x), dev(wr), dev(b)]
+        assert hip.kernel_name(hip.OP_CONV_IM2COL, out, srcs, p14).startswith(kern)
+        hip.run_checked(hip.OP_CONV_IM2COL, out, srcs, p14)
+        outs.append(host(out))
+    ref = orc.conv2d_f64(x, w, b, 2, 1, act)
+    assert np.isfinite(outs[0]).all()
+    assert normwise(outs[0], ref) < TOL and normwise(outs[1], ref) < TOL
+
+
 # ---------------------------------------------------------------- fused F(4,3) conv (op 17)
 def hip_wg4_conv(hip, x, w, b, act):
     _, wg4 = hip.repack_conv(w)
