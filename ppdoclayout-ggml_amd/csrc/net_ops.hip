@@ -794,9 +794,11 @@ hipError_t attention(const float *q, int ldq, const float *k, int ldk, const flo
     if (T < 1 || T > kAttWaves * kAttCPW * 32 || ldk % 4 || ldv % 4 || ldq % 4 ||
         (((uintptr_t)k | (uintptr_t)v | (uintptr_t)q) & 15))
         return hipErrorInvalidValue;
-    // 16 queries per block unless PPDL_ATT16=0
+    // 16 queries per block for the decoder's 300 tokens (PPDL_ATT16=0: never);
+    // with 625 tokens (AIFI) the 32-query kernel is faster in the graph
+    // (15.4 against 18.9 us: each wave already holds 3 key chunks)
     const char *e16 = getenv("PPDL_ATT16");
-    if (!(e16 && e16[0] == '0'))
+    if (!(e16 && e16[0] == '0') && T <= 320)
         hipLaunchKernelGGL(k_attention16, dim3((T + kA16Q - 1) / kA16Q, kNH), dim3(kAttThreads), 0, s, q, ldq, k, ldk,
                            v, ldv, out, ldo, T, 1.0f / sqrtf((float)kHD));
     else
