@@ -1757,7 +1757,49 @@ __global__ __launch_bounds__(WV * 64) void k_gemm_small16(GemmArgs g, int tiles_
     const float *__restrict__ B = g.B + (int64_t)bz * g.sB;
     const int mc = min(m0 + l16, M - 1), nc0 = min(n0 + l16, N - 1), nc1 = min(n0 + 16 + l16, N - 1);
     const int nchunk = K / KC;
-    const float4 xr = AMODE == 2 ? ld4(A + (uint32_t)(mc * lda)) : float4{0.0f, 0.0f, 0.0f, 0.0f};
+    float4 xr = AMODE >= 2 ? ld4(A + (uint32_t)(mc * lda)) : float4{0.0f, 0.0f, 0.0f, 0.0f};
+    if constexpr (AMODE == 3) {
+        // the previous layer's last box-head linear and the box refinement:
+        // d_j = box_b[j] + box_h[row] . box_w[:, j] over box_k = 256, each of
+        // the block's 32 threads per row taking 8 k (wave w, group g: k from
+        // 8 (4 w + g)), summed over the lane groups then the waves in order
+        static_assert(WV == 8, "32 threads x 8 k per row");
+        __shared__ float bsum[WV][16][4];
+        const int kb = 8 * (4 * wave + grp);
+        const float *hr = g.box_h + (uint32_t)(mc * g.box_ldh + kb);
+        const float4 h0 = ld4(hr), h1 = ld4(hr + 4);
+        const float hv[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
+        float d[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const float4 w = ld4(g.box_w + 4 * (kb + j));
+            d[0] = fmaf(hv[j], w.x, d[0]);
+            d[1] = fmaf(hv[j], w.y, d[1]);
+            d[2] = fmaf(hv[j], w.z, d[2]);
+            d[3] = fmaf(hv[j], w.w, d[3]);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            d[j] += __shfl_xor(d[j], 16);
+            d[j] += __shfl_xor(d[j], 32);
+        }
+        if (grp == 0)
+#pragma unroll
+            for (int j = 0; j < 4; j++) bsum[wave][l16][j] = d[j];
+        __syncthreads();
+        float t4[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            float sacc = 0.0f;
+#pragma unroll
+            for (int w = 0; w < WV; w++) sacc += bsum[w][l16][j];
+            t4[j] = sacc + g.box_b[j];
+        }
+        xr = make_float4(refine_box(t4[0], xr.x), refine_box(t4[1], xr.y), refine_box(t4[2], xr.z),
+                         refine_box(t4[3], xr.w));
+        if (n0 == 0 && wave == 0 && grp == 0 && m0 + l16 < M)
+            *reinterpret_cast<float4 *>(g.box_out + (uint32_t)(4 * (m0 + l16))) = xr;
+    }
     // prologue add (row-major A): a_add has A's layout; whole 32-column
     // tiles at or past a_add_n skip it
     const float *__restrict__ A2 = PRE ? g.a_add + (int64_t)bz * g.sA : nullptr;
@@ -1768,7 +1810,7 @@ __global__ __launch_bounds__(WV * 64) void k_gemm_small16(GemmArgs g, int tiles_
 #pragma unroll
         for (int h = 0; h < 2; h++) {
             const int k4 = k8 + 4 * h;
-            if (AMODE == 2) {
+            if (AMODE >= 2) {
                 const float4 w0 = ld4(g.a_w4 + k4), w1 = ld4(g.a_w4 + K + k4);
                 const float4 w2 = ld4(g.a_w4 + 2 * K + k4), w3 = ld4(g.a_w4 + 3 * K + k4);
                 const float4 bb = ld4(g.a_b4 + k4);
@@ -1926,7 +1968,9 @@ hipError_t launch_small16(const GemmArgs &g, int amode, hipStream_t s) {
     const dim3 grid((unsigned)total);
     // 8 waves with the computed A (16 would cap each wave at 128 registers:
     // spills); the row norm needs one 32-k chunk per wave
-    if (amode == 2) hipLaunchKernelGGL((k_gemm_small16<2, 8, false, false>), grid, dim3(512), 0, s, g, tiles_m, tmn);
+    if (amode == 2 && g.box_h)
+        hipLaunchKernelGGL((k_gemm_small16<3, 8, false, false>), grid, dim3(512), 0, s, g, tiles_m, tmn);
+    else if (amode == 2) hipLaunchKernelGGL((k_gemm_small16<2, 8, false, false>), grid, dim3(512), 0, s, g, tiles_m, tmn);
     else if (g.ln_g && g.a_add)
         hipLaunchKernelGGL((k_gemm_small16<1, 8, true, true>), grid, dim3(512), 0, s, g, tiles_m, tmn);
     else if (g.ln_g) hipLaunchKernelGGL((k_gemm_small16<1, 8, true, false>), grid, dim3(512), 0, s, g, tiles_m, tmn);
@@ -2253,6 +2297,13 @@ hipError_t dispatch(const GemmArgs &g_in, const GemmWorkspace &ws, hipStream_t s
         if (BMODE != 0 || !g.a_rowmajor || g.a_add || !g.a_b4 || g.lda != 4 || g.K % 4 != 0 || !a16(g.A) ||
             !a16(g.a_w4) || !a16(g.a_b4))
             return hipErrorInvalidValue;
+        if (g.box_h) {
+            // the box prologue exists in the 16 x 32 kernel only
+            const bool box_ok = small16_ok(g, 2) && g.box_k == 256 && g.box_ldh % 4 == 0 && g.box_ldh >= 256 &&
+                                a16(g.box_h) && a16(g.box_w) && g.box_b && g.box_out && a16(g.box_out) &&
+                                (int64_t)g.M * g.box_ldh < 0x7fffffff;
+            return box_ok ? launch_small16(g, 2, s) : hipErrorInvalidValue;
+        }
         return launch_small<2>(g, s);
     }
     const GemmPlan p = gemm_plan(g, ws.bytes, BMODE == 1);
@@ -2338,7 +2389,8 @@ std::string gemm_kernel_name(const GemmArgs &g, int64_t ws_bytes, bool im2col) {
     if (im2col && k2q_ok(g)) return "k_conv_k2q<" + std::to_string(g.IC) + (g.M <= 16 ? ", 1>" : ", 2>");
     if (im2col && k3s2q_ok(g)) return std::string("k_conv_k3s2q<64, ") + (g.M <= 16 ? "1>" : "2>");
     if (im2col && frag_ok(g)) return "k_conv_frag<" + std::to_string(frag_waves(g)) + ">";
-    if (g.a_w4 && small16_ok(g, 2)) return "k_gemm_small16<2, 8, false, false>";
+    if (g.a_w4 && small16_ok(g, 2))
+        return g.box_h ? "k_gemm_small16<3, 8, false, false>" : "k_gemm_small16<2, 8, false, false>";
     if (g.a_w4) return "k_gemm_small<2, " + std::to_string(small_waves(g.K, small_tiles(g))) + ", false>";
 
     const GemmPlan p = gemm_plan(g, ws_bytes, im2col);

@@ -352,7 +352,8 @@ class Net {
             float *ln_out = nullptr);
     Seq ln(const Seq &a, const float *b, const std::string &name, float *out = nullptr, int out_chw = 0);
     Seq mlp3(const Seq &x, const std::string &pfx);
-    Seq lin_in4(const Seq &x, const std::string &first, const std::string &second, int act);
+    Seq lin_in4(const Seq &x, const std::string &first, const std::string &second, int act,
+                const Seq *box_h = nullptr, float *box_out = nullptr);
     Seq mha(const Seq &x, const float *pos, const std::string &pfx, float *out, const float *resid);
     void hg_block(const Img &cat, int cin, const std::string &pfx, bool light, int mid, Img *y, float *out,
                   const float *resid);
@@ -746,7 +747,11 @@ Seq Net::ln(const Seq &a, const float *b, const std::string &name, float *out, i
 // second(relu(first(x))) for a 4-column x (the query-position MLP,
 // :824-826) as one GEMM: the 4-in ReLU layer is computed in the second
 // layer's A-operand loader, so its 300 x 512 hidden rows never reach memory
-Seq Net::lin_in4(const Seq &x, const std::string &first, const std::string &second, int act) {
+// With box_h: x is the previous layer's reference boxes and the GEMM first
+// applies that layer's last box-head linear (bbox_head.2 on box_h) and the
+// refinement to them in its loader, storing the refined boxes to box_out.
+Seq Net::lin_in4(const Seq &x, const std::string &first, const std::string &second, int act, const Seq *box_h,
+                 float *box_out) {
     const auto &n0 = shape(first + ".weight");   // (4, hidden)
     const auto &n1 = shape(second + ".weight");  // (hidden, out)
     if ((x.D != 4 || n0[0] != 4 || n1[0] != n0[1]) && bad_node_.empty()) bad_node_ = second + " (feature mismatch)";
@@ -769,6 +774,16 @@ Seq Net::lin_in4(const Seq &x, const std::string &first, const std::string &seco
     g.K = hid;
     g.batch = 1;
     g.act = act;
+    if (box_h) {
+        const auto &nb = shape("bbox_head.2.weight");  // (256, 4)
+        if ((nb[0] != box_h->D || nb[1] != 4) && bad_node_.empty()) bad_node_ = "bbox_head.2 (feature mismatch)";
+        g.box_h = box_h->d;
+        g.box_ldh = box_h->ld;
+        g.box_k = box_h->D;
+        g.box_w = W("bbox_head.2.wt");
+        g.box_b = W("bbox_head.2.bias");
+        g.box_out = box_out;
+    }
     gemm(second, g);
     return y;
 }
@@ -1070,9 +1085,24 @@ bool Net::build(bool dumps, std::string *err) {
     Seq xq = target;
     const char *dln = getenv("PPDL_DEC_LN");
     const bool fused_ln = !(dln && dln[0] == '0');
+    // Layers 1-5 refine the boxes of the previous layer inside their
+    // query-position GEMM (bbox_head.2 + refinement in its loader, the
+    // refined boxes stored to a buffer of their own); the last layer's
+    // bbox_head.2 writes the result boxes.  PPDL_BOX_FUSE=0: every layer's
+    // bbox_head.2 refines boxes_ in place.
+    const char *ebf = getenv("PPDL_BOX_FUSE");
+    const bool box_fuse = !(ebf && ebf[0] == '0');
+    Seq bh_prev;
     for (int i = 0; i < 6; i++) {
         const std::string dp = "dec" + std::to_string(i);
-        Seq qpos = lin_in4(ref, "qpos.0", "qpos.1", kActNone);
+        Seq qpos;
+        if (box_fuse && i > 0) {
+            float *ref_new = alloc((int64_t)NQ * 4);
+            qpos = lin_in4(ref, "qpos.0", "qpos.1", kActNone, &bh_prev, ref_new);
+            ref = Seq{ref_new, NQ, 4, 4};
+        } else {
+            qpos = lin_in4(ref, "qpos.0", "qpos.1", kActNone);
+        }
         // The post-residual layer norms (ln1..ln3) run in the A loader of the
         // GEMM that consumes them, which also stores the normed rows for
         // the residual add two GEMMs later: no layer-norm launches
@@ -1110,7 +1140,8 @@ bool Net::build(bool dumps, std::string *err) {
         static const char *hn[6] = {"hidden0", "hidden1", "hidden2", "hidden3", "hidden4", "hidden5"};
         dump(hn[i], xq.d, {kDM, NQ});
         Seq bh = lin(bh0, "bbox_head.1", kActRelu);
-        lin(bh, "bbox_head.2", kActNone, boxes_, boxes_, 3);
+        if (box_fuse && i < 5) bh_prev = bh;
+        else lin(bh, "bbox_head.2", kActNone, boxes_, ref.d, 3);  // boxes_ = refine(delta, ref)
     }
 
     // ---- heads (:865-876)

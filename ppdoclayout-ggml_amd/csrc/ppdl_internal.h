@@ -96,6 +96,16 @@ struct GemmArgs {
     const float *ln_g;
     const float *ln_b;
     float *ln_out;
+    // Box-refinement prologue (with a_w4, small-GEMM kernel): with box_h set,
+    // the 4-column X of row m is refine(box_b + box_h[m] . box_w, A[m]) (the
+    // previous layer's box head: box_h [M][box_k] row-major with row stride
+    // box_ldh, box_w [box_k][4], box_k == 256), and the blocks of the first
+    // column tile store those rows to box_out ([M][4]).
+    const float *box_h;
+    const float *box_w;
+    const float *box_b;
+    float *box_out;
+    int box_ldh, box_k;
 };
 
 // act codes of the GEMM epilogue and the elementwise kernels
