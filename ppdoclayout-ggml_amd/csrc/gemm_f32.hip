@@ -1974,8 +1974,19 @@ hipError_t launch_small16(const GemmArgs &g, int amode, hipStream_t s) {
     else if (g.ln_g && g.a_add)
         hipLaunchKernelGGL((k_gemm_small16<1, 8, true, true>), grid, dim3(512), 0, s, g, tiles_m, tmn);
     else if (g.ln_g) hipLaunchKernelGGL((k_gemm_small16<1, 8, true, false>), grid, dim3(512), 0, s, g, tiles_m, tmn);
-    else if (g.a_add) hipLaunchKernelGGL((k_gemm_small16<1, 16, false, true>), grid, dim3(1024), 0, s, g, tiles_m, tmn);
-    else hipLaunchKernelGGL((k_gemm_small16<1, 16, false, false>), grid, dim3(1024), 0, s, g, tiles_m, tmn);
+    // one 32-k chunk per wave at K = 256 (8 waves; 16 left half of them
+    // idle), two or more at K >= 512 (16 waves); PPDL_SMALL16_WV16=1 keeps 16
+    else {
+        const char *ew = getenv("PPDL_SMALL16_WV16");
+        const bool w8 = g.K <= 8 * kSmallKC && !(ew && ew[0] == '1');
+        if (g.a_add && w8)
+            hipLaunchKernelGGL((k_gemm_small16<1, 8, false, true>), grid, dim3(512), 0, s, g, tiles_m, tmn);
+        else if (g.a_add)
+            hipLaunchKernelGGL((k_gemm_small16<1, 16, false, true>), grid, dim3(1024), 0, s, g, tiles_m, tmn);
+        else if (w8)
+            hipLaunchKernelGGL((k_gemm_small16<1, 8, false, false>), grid, dim3(512), 0, s, g, tiles_m, tmn);
+        else hipLaunchKernelGGL((k_gemm_small16<1, 16, false, false>), grid, dim3(1024), 0, s, g, tiles_m, tmn);
+    }
     return hipGetLastError();
 }
 
@@ -2400,8 +2411,12 @@ std::string gemm_kernel_name(const GemmArgs &g, int64_t ws_bytes, bool im2col) {
         const int lc = gemm_lt_pick(gv, 8 * cus_per_xcd(), lt_wanted(gv, p));
         if (lc >= 0) return gemm_lt_name(lc);
     }
-    if (g.a_rowmajor && (g.ln_g || p.cfg == kCfgSmall) && small16_ok(g, 1))
-        return std::string("k_gemm_small16<1, ") + (g.ln_g ? "8, true, " : "16, false, ") + (g.a_add ? "true>" : "false>");
+    if (g.a_rowmajor && (g.ln_g || p.cfg == kCfgSmall) && small16_ok(g, 1)) {
+        const char *ew = getenv("PPDL_SMALL16_WV16");
+        const bool w8 = g.ln_g || (g.K <= 8 * kSmallKC && !(ew && ew[0] == '1'));
+        return std::string("k_gemm_small16<1, ") + (w8 ? "8, " : "16, ") + (g.ln_g ? "true, " : "false, ") +
+               (g.a_add ? "true>" : "false>");
+    }
     if (g.ln_g) return "k_gemm_small_ln<" + std::to_string(g.K / kSmallKC) + (g.a_add ? ", true>" : ", false>");
     if (p.cfg == kCfgSmall)
         return std::string("k_gemm_small<") + (g.a_rowmajor ? "1, " : "0, ") +
