@@ -1974,11 +1974,12 @@ hipError_t launch_small16(const GemmArgs &g, int amode, hipStream_t s) {
     else if (g.ln_g && g.a_add)
         hipLaunchKernelGGL((k_gemm_small16<1, 8, true, true>), grid, dim3(512), 0, s, g, tiles_m, tmn);
     else if (g.ln_g) hipLaunchKernelGGL((k_gemm_small16<1, 8, true, false>), grid, dim3(512), 0, s, g, tiles_m, tmn);
-    // one 32-k chunk per wave at K = 256 (8 waves; 16 left half of them
-    // idle), two or more at K >= 512 (16 waves); PPDL_SMALL16_WV16=1 keeps 16
+    // 8 waves: at K = 256 one 32-k chunk each (16 left half of them idle:
+    // graph -13 us), at K = 1024 four each (-4 us against 16 waves with
+    // two); PPDL_SMALL16_WV16=1 keeps 16
     else {
         const char *ew = getenv("PPDL_SMALL16_WV16");
-        const bool w8 = g.K <= 8 * kSmallKC && !(ew && ew[0] == '1');
+        const bool w8 = !(ew && ew[0] == '1');
         if (g.a_add && w8)
             hipLaunchKernelGGL((k_gemm_small16<1, 8, false, true>), grid, dim3(512), 0, s, g, tiles_m, tmn);
         else if (g.a_add)
@@ -2413,7 +2414,7 @@ std::string gemm_kernel_name(const GemmArgs &g, int64_t ws_bytes, bool im2col) {
     }
     if (g.a_rowmajor && (g.ln_g || p.cfg == kCfgSmall) && small16_ok(g, 1)) {
         const char *ew = getenv("PPDL_SMALL16_WV16");
-        const bool w8 = g.ln_g || (g.K <= 8 * kSmallKC && !(ew && ew[0] == '1'));
+        const bool w8 = g.ln_g || !(ew && ew[0] == '1');
         return std::string("k_gemm_small16<1, ") + (w8 ? "8, " : "16, ") + (g.ln_g ? "true, " : "false, ") +
                (g.a_add ? "true>" : "false>");
     }
