@@ -1946,7 +1946,9 @@ __global__ __launch_bounds__(WV * 64) void k_gemm_small16(GemmArgs g, int tiles_
 // PPDL_SMALL16_T the block bound, for A/B runs; read per call).  Same-process
 // graph A/B: K >= 512 (fc2, qpos.1) 37 us per image faster; K >= 256 (also
 // sa.o, ca.op, the box and mask-query heads) 25 us more; K >= 32 7 us slower
-// than K >= 256; a bound of 400 instead of 128 blocks (adds sa.qkv, fc1) 3 us.
+// than K >= 256; a bound of 400 instead of 128 blocks (adds sa.qkv, fc1) 3 us;
+// 700 (adds AIFI's qkv and fc1, 480 and 640 tiles) 3.4 us once the kernel ran
+// 8 waves (with 16 it had been 8 us slower).
 bool small16_ok(const GemmArgs &g, int amode) {
     const char *e = getenv("PPDL_SMALL16");
     if (e && e[0] == '0') return false;
@@ -1954,7 +1956,7 @@ bool small16_ok(const GemmArgs &g, int amode) {
     const auto a16 = [](const void *q) { return (((uintptr_t)q) & 15) == 0; };
     const int64_t kmin = (e && *e && e[0] != '0') ? atoi(e) : 256;
     const char *et = getenv("PPDL_SMALL16_T");
-    const int64_t tmax = (et && *et) ? atoi(et) : 400;
+    const int64_t tmax = (et && *et) ? atoi(et) : 700;
     return (amode == 1 || amode == 2) && g.K >= kmin && g.K % kSmallKC == 0 && t32 < tmax && !g.c_trans && !g.bits &&
            (amode == 1 || !g.ln_g) && (!g.ln_g || g.K == 8 * kSmallKC) &&
            (!g.a_add || (a16(g.a_add) && g.a_add_n % 32 == 0)) && g.lda % 4 == 0 && a16(g.A) &&
