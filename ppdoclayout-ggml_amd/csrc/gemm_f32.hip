@@ -2063,14 +2063,14 @@ GemmPlan plan_auto(int M, int N, int K, int batch, bool im2col) {
     // network sweep (200/40, 400/80, 700/160 tiles/MB): 400/80 was fastest.
     const int64_t t64 = (int64_t)((M + 63) / 64) * ((N + 63) / 64) * batch;
     const int64_t reread = 4 * ((int64_t)M * K * ((N + 31) / 32) + (int64_t)K * N * ((M + 31) / 32)) * batch;
-    static const int64_t small_t64 = env_int("PPDL_SMALL_T64", 400);
-    static const int64_t small_mb = env_int("PPDL_SMALL_MB", 80);
+    const int64_t small_t64 = env_int("PPDL_SMALL_T64", 400);  // read per plan: in-process A/B
+    const int64_t small_mb = env_int("PPDL_SMALL_MB", 80);
     if (!im2col && t64 < small_t64 && reread <= (small_mb << 20)) return GemmPlan{kCfgSmall, 1};
     GemmPlan p{M <= 32 ? 5 : 3, 1};
     const int nk = (K + kBK - 1) / kBK;
     const int64_t tiles = tiles_of(p.cfg, M, N, batch);
-    static const int64_t target = env_int("PPDL_SPLIT_BLOCKS", 1000);
-    static const int64_t min_kt = env_int("PPDL_SPLIT_MIN_KT", 6);
+    const int64_t target = env_int("PPDL_SPLIT_BLOCKS", 1000);
+    const int64_t min_kt = env_int("PPDL_SPLIT_MIN_KT", 6);
     int64_t want = target / (tiles > 0 ? tiles : 1);
     const int64_t cap = nk / min_kt;
     if (want > cap) want = cap;
