@@ -172,23 +172,40 @@ __device__ __forceinline__ void gemm_epilogue(const f32x16 (&acc)[TM][TN], const
         return v;
     };
     if (!g.c_trans) {
+        // the store loop once per common activation (none, ReLU, SiLU), so
+        // the unrolled loop a launch runs carries one activation's code
+        auto store = [&](auto actc) {
+            constexpr int A = decltype(actc)::value;
+            auto epa = [&](float v, float bval, int64_t idx) {
+                if (bias) v += bval;
+                if (add_mode == 1) v += Ad[idx];
+                v = act_t<A>(v, act);
+                if (add_mode == 2) v += Ad[idx];
+                else if (add_mode == 3) v = refine_box(v, Ad[idx]);
+                return v;
+            };
 #pragma unroll
-        for (int j = 0; j < TN; j++) {
-            const int n = nw + j * 32 + l32;
-            if (n < N) {
+            for (int j = 0; j < TN; j++) {
+                const int n = nw + j * 32 + l32;
+                if (n < N) {
 #pragma unroll
-                for (int i = 0; i < TM; i++) {
+                    for (int i = 0; i < TM; i++) {
 #pragma unroll
-                    for (int r = RB; r < RB + RN; r++) {
-                        const int m = mw + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                        if (m < M) {
-                            const int64_t idx = (int64_t)m * g.ldc + n;
-                            C[idx] = epi(acc[i][j][r], bias ? bias_of(i, r, m, n) : 0.0f, idx);
+                        for (int r = RB; r < RB + RN; r++) {
+                            const int m = mw + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                            if (m < M) {
+                                const int64_t idx = (int64_t)m * g.ldc + n;
+                                C[idx] = epa(acc[i][j][r], bias ? bias_of(i, r, m, n) : 0.0f, idx);
+                            }
                         }
                     }
                 }
             }
-        }
+        };
+        if (act == kActNone) store(std::integral_constant<int, kActNone>{});
+        else if (act == kActRelu) store(std::integral_constant<int, kActRelu>{});
+        else if (act == kActSilu) store(std::integral_constant<int, kActSilu>{});
+        else store(std::integral_constant<int, -1>{});
     } else {
         // C[n][m]: registers 4g..4g+3 hold 4 consecutive m of one n
         const bool vec_ok = (g.ldc % 4 == 0) && ((((uintptr_t)C) & 15) == 0) &&
