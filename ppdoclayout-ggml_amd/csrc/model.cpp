@@ -978,9 +978,19 @@ bool Net::build(bool dumps, std::string *err) {
     dump("mask_feat", mask_feat);
     main_lane();
 
-    // ---- decoder inputs (:791-801): 1x1 projections written token-major
-    // into one (13125, 256) source, level after level
-    Seq source{alloc((int64_t)NTOK * kDM), NTOK, kDM, kDM};
+    // ---- decoder inputs (:791-801): 1x1 projections written channel-major
+    // into one (256, LDT) sourceT, level after level along the token axis.
+    // Channel-major makes sourceT the k-major A operand of the value and
+    // enc_out projections, whose GEMMs then run on the DMA-staged kernel (a
+    // row-major A has no DMA loader); the tokens are padded to LDT = 13128
+    // so that M and the leading dimension are multiples of 4.  The padding
+    // columns hold no data: the GEMMs compute rows 13125..13127 from them and
+    // nothing reads those rows.  PPDL_SOURCE_TM=1 keeps the token-major
+    // source and the row-major GEMMs (A/B runs, tests).
+    const char *etm = getenv("PPDL_SOURCE_TM");
+    const bool src_tm = etm && etm[0] == '1';
+    constexpr int LDT = (NTOK + 3) / 4 * 4;
+    float *sbuf = alloc((int64_t)LDT * kDM);
     {
         const Img lv[3] = {f8, n16, n32};
         const int start[3] = {0, 10000, 12500};
@@ -992,37 +1002,79 @@ bool Net::build(bool dumps, std::string *err) {
             g.lda = kDM;
             g.B = lv[l].d;
             g.ldb = P;
-            g.C = source.d + (int64_t)start[l] * kDM;
-            g.ldc = kDM;
-            g.c_trans = 1;
+            g.C = src_tm ? sbuf + (int64_t)start[l] * kDM : sbuf + start[l];
+            g.ldc = src_tm ? kDM : LDT;
+            g.c_trans = src_tm ? 1 : 0;
             g.bias = W(nm + ".bias");
             g.M = kDM;
             g.N = P;
             g.K = lv[l].C;
             g.batch = 1;
-            gemm(nm, g, 1);  // a 1x1 conv (src/ppdoclayout.cpp:786-788) stored token-major
+            gemm(nm, g, 1);  // a 1x1 conv (src/ppdoclayout.cpp:786-788)
         }
     }
-    dump("source", source.d, {kDM, NTOK});
+    // the linear `name` of a source-shaped x (either layout); y has LDT rows
+    const auto lin_src = [&](const float *x, const std::string &name, float *out) {
+        if (src_tm) return lin(Seq{const_cast<float *>(x), NTOK, kDM, kDM}, name, kActNone, out);
+        const auto &ne = shape(name + ".weight");  // (in, out)
+        const int nout = (int)ne[1];
+        if ((int)ne[0] != kDM && bad_node_.empty()) bad_node_ = name + " (feature mismatch)";
+        Seq y{out ? out : alloc((int64_t)LDT * nout), NTOK, nout, nout};
+        GemmArgs g{};
+        g.A = x;  // k-major: A[k][m] = x[k * LDT + m]
+        g.lda = LDT;
+        g.B = W(name + ".wt");
+        g.ldb = nout;
+        g.C = y.d;
+        g.ldc = nout;
+        g.bias = W(name + ".bias");
+        g.bias_n = 1;
+        g.M = LDT;
+        g.N = nout;
+        g.K = kDM;
+        g.batch = 1;
+        gemm(name, g);
+        return y;
+    };
+    if (want_dumps_) {
+        if (src_tm) {
+            dump("source", sbuf, {kDM, NTOK});
+        } else {
+            float *tm = alloc((int64_t)LDT * kDM);
+            node("source.tm", 1, [=](hipStream_t st) { return ok(transpose(sbuf, tm, kDM, LDT, kDM, st)); });
+            dump("source", tm, {kDM, NTOK});
+        }
+    }
     // value projections of all six decoder layers at once (layer i: columns
     // 256i..256i+255), on lane 2 until the first deformable attention
     fork(2);
-    const Seq vcat = lin(source, "dec.ca.vp", kActNone);
+    const Seq vcat = lin_src(sbuf, "dec.ca.vp", nullptr);
     main_lane();
     // memory = source * valid (:797), consumed only by enc_out.l.  valid is 0
     // or 1 per token, so enc_out.l(memory) equals enc_out.l(source) on valid
     // rows and the bias row on masked ones (a zero row through the GEMM: every
     // product is a zero, as long as source is finite): the GEMM runs on
     // source and the LayerNorm takes the bias for masked rows.  PPDL_MEMORY=1
-    // keeps the multiply as its own node.
+    // keeps the multiply as its own node (channel-major source: through a
+    // token-major copy and back, both exact).
     const char *emem = getenv("PPDL_MEMORY");
     Seq om;
     if (emem && emem[0] == '1') {
-        Seq memory{alloc((int64_t)NTOK * kDM), NTOK, kDM, kDM};
-        node("memory", 1, [=](hipStream_t st) { return ok(mul_rows(source.d, valid_, memory.d, NTOK, kDM, st)); });
-        om = ln(lin(memory, "enc_out.l", kActNone), nullptr, "enc_out.ln");
+        float *mem = alloc((int64_t)LDT * kDM);
+        if (src_tm) {
+            node("memory", 1, [=](hipStream_t st) { return ok(mul_rows(sbuf, valid_, mem, NTOK, kDM, st)); });
+        } else {
+            float *tm = alloc((int64_t)LDT * kDM), *mt = alloc((int64_t)LDT * kDM);
+            node("memory", 3, [=](hipStream_t st) {
+                hipError_t e = transpose(sbuf, tm, kDM, LDT, kDM, st);
+                if (e == hipSuccess) e = mul_rows(tm, valid_, mt, NTOK, kDM, st);
+                if (e == hipSuccess) e = transpose(mt, mem, LDT, kDM, LDT, st);
+                return ok(e);
+            });
+        }
+        om = ln(lin_src(mem, "enc_out.l", nullptr), nullptr, "enc_out.ln");
     } else {
-        const Seq eo = lin(source, "enc_out.l", kActNone);
+        const Seq eo = lin_src(sbuf, "enc_out.l", nullptr);
         om = Seq{alloc((int64_t)NTOK * kDM), NTOK, kDM, kDM};
         const float *gm = W("enc_out.ln.weight"), *bt = W("enc_out.ln.bias"), *fill = W("enc_out.l.bias");
         const float *mask = valid_;

@@ -302,13 +302,15 @@ def test_exact_variants_match_default(gpu, model, image, monkeypatch, knob):
         ctx.close()
 
 
-@pytest.mark.parametrize("knob", ["PPDL_ATT16=0", "PPDL_BOX_FUSE=0"])
+@pytest.mark.parametrize("knob", ["PPDL_ATT16=0", "PPDL_BOX_FUSE=0", "PPDL_SOURCE_TM=1"])
 def test_numeric_variants_match_default(gpu, model, image, monkeypatch, knob):
     """Graph variants with another summation order: the attention with 32
     queries per block (v_mfma_f32_32x32x2f32) against the default 16-query
     kernel (v_mfma_f32_16x16x4f32), and each layer's box-head output linear
     + refinement as its own GEMM against the default, where the next
-    layer's query-position GEMM computes it in its loader.  Raw outputs
+    layer's query-position GEMM computes it in its loader; and the
+    token-major source with row-major value / enc_out GEMMs against the
+    default channel-major source on the DMA-staged kernel.  Raw outputs
     within the network tolerance, the same top-300 selection up to swaps of
     tied scores."""
     import ppdoclayout as P
