@@ -379,8 +379,9 @@ class Net {
     int lane_ = 0;
     // Branches on separate streams (PPDL_GRAPH_LANES=1).  Off by default:
     // measured on MI355X / ROCm 7, the captured graph with two side branches
-    // replays ~0.14 ms slower than the same nodes on one stream, more than
-    // the ~0.2 ms of overlappable work it gains.
+    // replays ~0.1 ms slower than the same nodes on one stream, more than
+    // the ~0.2 ms of overlappable work it gains (the value projection's
+    // branch alone: ~0.15 ms slower).
     bool multi_lane_ = false;
     hipStream_t lanes_[kLanes] = {};  // lanes_[0] is stream_
     std::vector<hipEvent_t> events_;
